@@ -1,0 +1,218 @@
+#!/usr/bin/env python3
+"""MoE-layer benchmark on one MI355X.
+
+Workload ("config 2"): Qwen3-Next-shaped MoE layer
+decode at batch 1 -- hidden 2048, 512 experts, top-10 renormalised softmax
+routing, expert ff 512 with SwiGLU, shared expert ff 512 with a sigmoid gate;
+routed and shared expert weights MLX-affine 4-bit g64 with bf16 scales and
+biases, F32 router.  A step is one MoE layer applied to one token.
+
+Cold-HBM protocol: 8 distinct layers (each with all 512 experts resident,
+~7.3 GB in total, far beyond the 256 MB Infinity Cache) are rotated step by
+step, every step on a fresh N(0,1) token.  Steps are captured into a HIP graph
+of 64 steps and replayed; the timed region is bracketed by stream
+synchronisation (hipEvents on the library's stream measure it).
+
+Output: one JSON line (see the driver contract) with the dominant kernel's
+roofline (algorithmic bytes / its hipEvent-measured average duration) and the
+CPU oracle timed on this host's cores.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "llama-rs-metal_amd")
+sys.path.insert(0, PKG)
+
+import numpy as np  # noqa: E402
+
+from hip_backend import BF16, BlockWeights, Gpu, Tensor, synth  # noqa: E402
+
+METRIC = ("MoE-layer tokens/s + achieved HBM GB/s (decode b=1) and MFMA util (prefill)")
+H, E, K, FF, FFS, BITS, GROUP = 2048, 512, 10, 512, 512, 4, 64
+# affine matrix bytes = out*in*bits/8 + 2*(out*in/group)*2 (bf16 scales + biases)
+MAT_BYTES = FF * H * BITS // 8 + 2 * (FF * H // GROUP) * 2          # 589,824
+EXPERT_BYTES_PER_TOKEN = K * 3 * MAT_BYTES + 3 * MAT_BYTES          # 19,464,192
+ROUTER_BYTES = H * E * 4 + H * 4                                    # F32 router + gate row
+GATEUP_BYTES = K * 2 * MAT_BYTES                                    # decode_gateup per launch
+HBM_PEAK = 8.0e12
+CHUNK = 64       # steps per captured graph
+LAYERS = 8       # distinct weight sets rotated
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_layer_tensors(seed):
+    """Host tensors of one config-2 layer (router F32 N(0,0.02); shared expert
+    quantised from N(0,0.02); routed experts uniform 4-bit codes with
+    N(0,0.02)-sized group scales -- see hip_backend.synth.random_affine)."""
+    s = seed * 100
+    router = Tensor.dense([H, E], synth.normal(s + 1, H * E, 0.0, 0.02))
+    experts = []
+    for i, dims in enumerate(([H, FF, E], [H, FF, E], [FF, H, E])):
+        n = int(np.prod(dims))
+        experts.append(Tensor.affine(dims, *synth.random_affine(s + 2 + i, n, BITS, GROUP, BF16),
+                                     BITS, GROUP, BF16))
+    shared = []
+    for i, dims in enumerate(([H, FFS], [H, FFS], [FFS, H])):
+        n = int(np.prod(dims))
+        shared.append(Tensor.affine(dims, *synth.quantize_affine(
+            synth.normal(s + 5 + i, n, 0.0, 0.02), BITS, GROUP, BF16), BITS, GROUP, BF16))
+    sgate = Tensor.dense([H], synth.normal(s + 8, H, 0.0, 0.02))
+    return router, experts, shared, sgate
+
+
+def upload_layer(gpu, tensors):
+    router, experts, shared, sgate = tensors
+    w = [gpu.weight_tensor(t) for t in [router, *experts]]
+    sh = tuple(gpu.weight_tensor(t) for t in shared)
+    return BlockWeights(w[0], w[1], w[2], w[3], K, True, sh, gpu.weight_tensor(sgate))
+
+
+def cpu_baseline(tensors, budget_s):
+    """The C oracle (single thread) on the same layer, bounded sample."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    router, experts, shared, sgate = tensors
+    spec = oracle.MoeSpec(router, experts[0], experts[1], experts[2], K, True, tuple(shared), sgate)
+    oracle.build() if not os.path.exists(oracle.LIB_PATH) else None
+    n, t0 = 0, time.perf_counter()
+    while True:
+        x = synth.normal(900000 + n, H).reshape(1, H)
+        oracle.moe_block(spec, x, 1)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 10000:
+            break
+    return {"value": n / el, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{n} config-2 decode tokens (layer 0 weights, seeds 900000+) through "
+                      f"oracle/moe_oracle.c orc_moe_block, single thread, {el:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=12800)
+    ap.add_argument("--warmup", type=int, default=640)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              f"(see DESIGN.md for how the MoE layer would shard)", file=sys.stderr)
+        sys.exit(2)
+    steps = max(CHUNK, (args.steps + CHUNK - 1) // CHUNK * CHUNK)
+    warm = max(CHUNK, (args.warmup + CHUNK - 1) // CHUNK * CHUNK)
+
+    gpu = Gpu(0)
+    log(f"[bench] device {gpu.name}; building {LAYERS} config-2 layers")
+    layers, host0 = [], None
+    for l in range(LAYERS):
+        t = make_layer_tensors(500 + l)
+        layers.append(upload_layer(gpu, t))
+        if l == 0:
+            host0 = t
+        log(f"[bench] layer {l} resident ({gpu.allocated_bytes() / 1e9:.2f} GB)")
+    xs = gpu.upload(synth.normal(4242, CHUNK * H))
+    outs = gpu.zeros(CHUNK * H)
+    ws = gpu.zeros(layers[0].workspace_elems(1))
+
+    def issue(b, j):
+        x = xs.view(j * H, H)
+        o = outs.view(j * H, H)
+        b.moe_block(layers[j % LAYERS], x, o, 1, ws)
+
+    # per-kernel durations (hipEvents around each launch, eager)
+    gpu.profile_reset()
+    gpu.profile(True)
+    with gpu.batch() as b:
+        for j in range(CHUNK):
+            issue(b, j)
+    prof = gpu.profile_read()
+    gpu.profile(False)
+    kernels = {k: v[1] / v[0] for k, v in prof.items()}
+    log("[bench] kernel averages (us): " + ", ".join(f"{k} {v * 1e6:.2f}" for k, v in kernels.items()))
+
+    # eager throughput (no graph) for reference
+    with gpu.batch() as b:
+        for j in range(CHUNK):
+            issue(b, j)
+    eager_s = b.seconds / CHUNK
+
+    cap = gpu.capture()
+    with cap as b:
+        for j in range(CHUNK):
+            issue(b, j)
+    graph = cap.graph
+    with gpu.batch() as b:
+        for _ in range(warm // CHUNK):
+            b.graph(graph)
+    log(f"[bench] warmup {warm} steps done")
+    t0 = time.perf_counter()
+    with gpu.batch() as b:
+        for _ in range(steps // CHUNK):
+            b.graph(graph)
+    wall = time.perf_counter() - t0
+    gpu_s = b.seconds
+    log(f"[bench] timed {steps} steps: {gpu_s * 1e3:.2f} ms (events), {wall * 1e3:.2f} ms (wall)")
+    elapsed = max(gpu_s, 1e-12)
+    per_step = elapsed / steps
+
+    dom = "decode_gateup"
+    dom_s = kernels.get(dom)
+    roof = None
+    if dom_s:
+        achieved = GATEUP_BYTES / dom_s / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9,
+                "unit": "GB/s", "frac": round(achieved * 1e9 / HBM_PEAK, 4), "traffic": None,
+                "kernel": dom, "algorithmic_bytes_per_launch": GATEUP_BYTES,
+                "avg_launch_us": round(dom_s * 1e6, 3)}
+        tpath = os.path.join(ROOT, "profiles", "traffic_decode_gateup.json")
+        if os.path.exists(tpath):
+            with open(tpath) as f:
+                tr = json.load(f)
+            roof["traffic"] = tr.get("bytes_per_launch")
+            roof["traffic_source"] = "profiles/traffic_decode_gateup.json"
+
+    layer_gbps = EXPERT_BYTES_PER_TOKEN / per_step / 1e9
+    result = {
+        "metric": METRIC,
+        "value": round(steps / elapsed, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warm,
+        "ms_per_step": round(per_step * 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "config2: Qwen3-Next MoE layer decode b=1 (h2048 E512 top10 "
+                               "ff512 + shared ff512, 4-bit g64 bf16, F32 router)",
+                   "layers_rotated": LAYERS, "graph_steps": CHUNK, "path": "fused decode"},
+        "layer_hbm": {"expert_bytes_per_token": EXPERT_BYTES_PER_TOKEN,
+                      "all_bytes_per_token": EXPERT_BYTES_PER_TOKEN + ROUTER_BYTES,
+                      "achieved_GBps": round(layer_gbps, 1),
+                      "frac": round(layer_gbps * 1e9 / HBM_PEAK, 4)},
+        "eager_ms_per_step": round(eager_s * 1e3, 6),
+        "kernels_us": {k: round(v * 1e6, 3) for k, v in kernels.items()},
+        "roofline": roof,
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        log("[bench] timing the CPU oracle")
+        result["cpu_baseline"] = cpu_baseline(host0, args.cpu_seconds)
+        result["cpu_baseline"]["host_cpus"] = os.cpu_count()
+    print(json.dumps(result), flush=True)
+    gpu.close()
+
+
+if __name__ == "__main__":
+    main()

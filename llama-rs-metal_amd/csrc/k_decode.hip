@@ -1,0 +1,472 @@
+// Fused single-token MoE decode: three launches per layer.
+//
+//   decode_pre     router GEMV (+logit bias) and, independent of routing, the
+//                  shared expert's gate/up/SwiGLU and its scalar gate input.
+//   decode_gateup  every block re-derives the top-k routing from the logits
+//                  (one wave, exact), then streams the selected experts'
+//                  gate/up rows and writes SwiGLU activations.
+//   decode_down    down rows of the K routed experts and the shared expert,
+//                  weighted combine, sigmoid shared gate and residual.
+//
+// Weight layout "chunk32": lane (sub, cl) of a wave owns 32 consecutive
+// elements (chunk cl) of row `sub`; a row of `in` elements spans in/32 lanes
+// (a power of two <= 64), so one wave instruction covers 64/(in/32) rows and
+// every lane issues one 8/16/32-byte load per affine row (2/4/8-bit), all
+// coalesced.  Each chunk lies inside one quantization group (group >= 32).
+// The activations a lane multiplies against stay in registers.
+#include "route.hpp"
+
+namespace moehip {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// 32 consecutive weight elements of one row as raw words.
+template <int BITS, int T>
+struct Chunk32 {
+    static constexpr int BYTES = BITS ? 4 * BITS : (T == 0 ? 128 : 64);
+    static constexpr int NW = BYTES / 4;
+    uint32_t w[NW];
+    __device__ __forceinline__ void load(const void *base, uint64_t chunk) {
+        const uint8_t *p = reinterpret_cast<const uint8_t *>(base) + chunk * BYTES;
+        if constexpr (NW >= 4) {
+#pragma unroll
+            for (int i = 0; i < NW / 4; i++) {
+                const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p) + i);
+                w[4 * i + 0] = v[0];
+                w[4 * i + 1] = v[1];
+                w[4 * i + 2] = v[2];
+                w[4 * i + 3] = v[3];
+            }
+        } else {
+            const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(p));
+            w[0] = v[0];
+            w[1] = v[1];
+        }
+    }
+    // sum_j value_j * x[j]; for affine rows value_j is the raw code.
+    __device__ __forceinline__ float dot(const float *x) const {
+        float d = 0.f;
+        if constexpr (BITS) {
+            constexpr int P = 32 / BITS;
+#pragma unroll
+            for (int i = 0; i < NW; i++) d += word_dot<BITS>(w[i], x + i * P);
+        } else if constexpr (T == 0) {
+#pragma unroll
+            for (int j = 0; j < 32; j++) d = fmaf(__uint_as_float(w[j]), x[j], d);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const float lo = T == 30 ? bf16_to_f32(w[i] & 0xffffu) : f16_to_f32(w[i] & 0xffffu);
+                const float hi = T == 30 ? bf16_to_f32(w[i] >> 16) : f16_to_f32(w[i] >> 16);
+                d = fmaf(lo, x[2 * i], d);
+                d = fmaf(hi, x[2 * i + 1], d);
+            }
+        }
+        return d;
+    }
+};
+
+// One lane's share of `R` rows: chunk loads (and group scale/bias loads) are
+// all issued before any arithmetic so R rows are in flight per lane.
+// rows[f] >= nrows marks an absent row (contributes 0).
+template <int BITS, int T, int R>
+__device__ __forceinline__ void lane_rows_dot(const WDesc &w, const uint64_t *grow, const bool *ok,
+                                              uint32_t cl, uint32_t C, const float *x, float xsum,
+                                              float *res) {
+    Chunk32<BITS, T> c[R];
+    float s[R], b[R];
+#pragma unroll
+    for (int f = 0; f < R; f++) {
+        if (ok[f]) {
+            c[f].load(w.data, grow[f] * C + cl);
+            if constexpr (BITS) {
+                const uint64_t g = (grow[f] * w.in + (uint64_t)cl * 32) >> w.gshift;
+                s[f] = load_scalar<T>(w.scales, g);
+                b[f] = load_scalar<T>(w.biases, g);
+            }
+        }
+    }
+#pragma unroll
+    for (int f = 0; f < R; f++) {
+        float v = 0.f;
+        if (ok[f]) {
+            if constexpr (BITS)
+                v = s[f] * c[f].dot(x) + b[f] * xsum;
+            else
+                v = c[f].dot(x);
+        }
+        res[f] = v;
+    }
+}
+
+// Single row of any kind (wave-uniform switch on the weight's kind).
+template <int ST>
+__device__ __forceinline__ float lane_row_dot_any(const WDesc &w, uint64_t grow, uint32_t cl,
+                                                  uint32_t C, const float *x, float xsum) {
+    const bool ok = true;
+    float r = 0.f;
+    switch (w.bits) {
+    case 2: lane_rows_dot<2, ST, 1>(w, &grow, &ok, cl, C, x, xsum, &r); break;
+    case 4: lane_rows_dot<4, ST, 1>(w, &grow, &ok, cl, C, x, xsum, &r); break;
+    case 8: lane_rows_dot<8, ST, 1>(w, &grow, &ok, cl, C, x, xsum, &r); break;
+    default:
+        if (w.type == 0)
+            lane_rows_dot<0, 0, 1>(w, &grow, &ok, cl, C, x, xsum, &r);
+        else if (w.type == 1)
+            lane_rows_dot<0, 1, 1>(w, &grow, &ok, cl, C, x, xsum, &r);
+        else
+            lane_rows_dot<0, 30, 1>(w, &grow, &ok, cl, C, x, xsum, &r);
+    }
+    return r;
+}
+
+// This lane's 32-element slice of the (optionally RMS-normalised) input.
+// RMSNorm (crates/metal-backend/src/shaders/elementwise.metal:31-46): the sum
+// of squares is reduced over the `width` lanes that span the row.
+__device__ __forceinline__ float load_x_chunk(const float *__restrict__ x,
+                                              const float *__restrict__ norm_w, float eps,
+                                              uint32_t h, uint32_t cl, int width, float *xr) {
+    const float4 *src = reinterpret_cast<const float4 *>(x + (uint64_t)cl * 32);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 v = src[i];
+        xr[4 * i + 0] = v.x;
+        xr[4 * i + 1] = v.y;
+        xr[4 * i + 2] = v.z;
+        xr[4 * i + 3] = v.w;
+    }
+    if (norm_w) {
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < 32; j++) ss += xr[j] * xr[j];
+        ss = subwave_sum(ss, width);
+        const float inv = 1.0f / sqrtf(ss / (float)h + eps);
+        const float4 *wv = reinterpret_cast<const float4 *>(norm_w + (uint64_t)cl * 32);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 v = wv[i];
+            xr[4 * i + 0] = xr[4 * i + 0] * inv * v.x;
+            xr[4 * i + 1] = xr[4 * i + 1] * inv * v.y;
+            xr[4 * i + 2] = xr[4 * i + 2] * inv * v.z;
+            xr[4 * i + 3] = xr[4 * i + 3] * inv * v.w;
+        }
+    }
+    float xsum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 32; j++) xsum += xr[j];
+    return xsum;
+}
+
+struct DecodeKArgs {
+    WDesc router, gate, up, down, sg, su, sd, sgi;
+    uint32_t has_shared, k, normalize;
+    uint32_t h, ff, ffs, E;
+    uint32_t lpr_h, lpr_f;  // lanes per row along h / along ff (powers of two <= 64)
+    uint32_t n_router_waves, n_shared_waves, n_gate_waves_per_expert;
+    const float *x, *norm_w, *logit_bias, *resid;
+    float eps;
+    float *out, *logits;
+    uint32_t *ids;
+    float *weights, *act, *sh_act, *sh_gate;
+};
+
+constexpr int kSharedFR = 2;  // shared ff indices per sub-wave in decode_pre
+constexpr int kGateFR = 4;    // routed ff indices per sub-wave in decode_gateup
+constexpr int kDownFR = 2;    // output rows per sub-wave in decode_down
+
+// ------------------------------------------------------------------ pre --
+template <int BR, int TR>
+__device__ __forceinline__ void router_item(const DecodeKArgs &a, uint32_t wave_id, uint32_t sub,
+                                            uint32_t cl, const float *xr, float xsum) {
+    // router GEMV rows (Batch::matmul(router), crates/model-runtime/src/execute.rs:220)
+    const uint32_t lpr = a.lpr_h, rpi = 64u / lpr;
+    const uint64_t e = (uint64_t)wave_id * rpi + sub;
+    const bool ok = e < a.E;
+    float v;
+    lane_rows_dot<BR, TR, 1>(a.router, &e, &ok, cl, a.h / 32, xr, xsum, &v);
+    v = subwave_sum(v, (int)lpr);
+    if (ok && cl == 0) a.logits[e] = a.logit_bias ? v + a.logit_bias[e] : v;
+}
+
+template <int BS, int ST>
+__device__ __forceinline__ void shared_item(const DecodeKArgs &a, uint32_t wave_id, uint32_t sub,
+                                            uint32_t cl, const float *xr, float xsum) {
+    // shared expert gate/up + SwiGLU (encode_dense, execute.rs:258-264)
+    const uint32_t lpr = a.lpr_h, rpi = 64u / lpr;
+    uint64_t rows[kSharedFR];
+    bool ok[kSharedFR];
+#pragma unroll
+    for (int f = 0; f < kSharedFR; f++) {
+        rows[f] = ((uint64_t)wave_id * kSharedFR + f) * rpi + sub;
+        ok[f] = rows[f] < a.ffs;
+    }
+    float g[kSharedFR], u[kSharedFR];
+    lane_rows_dot<BS, ST, kSharedFR>(a.sg, rows, ok, cl, a.h / 32, xr, xsum, g);
+    lane_rows_dot<BS, ST, kSharedFR>(a.su, rows, ok, cl, a.h / 32, xr, xsum, u);
+#pragma unroll
+    for (int f = 0; f < kSharedFR; f++) {
+        const float gv = subwave_sum(g[f], (int)lpr), uv = subwave_sum(u[f], (int)lpr);
+        if (ok[f] && cl == 0) a.sh_act[rows[f]] = gv / (1.0f + expf(-gv)) * uv;
+    }
+}
+
+template <int ST>
+__global__ __launch_bounds__(256) void decode_pre_kernel(DecodeKArgs a) {
+    const int lane = threadIdx.x & 63;
+    uint32_t wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const uint32_t lpr = a.lpr_h, sub = lane / lpr, cl = lane % lpr;
+    float xr[32];
+    const float xsum = load_x_chunk(a.x, a.norm_w, a.eps, a.h, cl, (int)lpr, xr);
+    if (wave_id < a.n_router_waves) {
+        const WDesc &r = a.router;
+        switch (r.bits) {
+        case 2: router_item<2, ST>(a, wave_id, sub, cl, xr, xsum); break;
+        case 4: router_item<4, ST>(a, wave_id, sub, cl, xr, xsum); break;
+        case 8: router_item<8, ST>(a, wave_id, sub, cl, xr, xsum); break;
+        default:
+            if (r.type == 0)
+                router_item<0, 0>(a, wave_id, sub, cl, xr, xsum);
+            else if (r.type == 1)
+                router_item<0, 1>(a, wave_id, sub, cl, xr, xsum);
+            else
+                router_item<0, 30>(a, wave_id, sub, cl, xr, xsum);
+        }
+        return;
+    }
+    wave_id -= a.n_router_waves;
+    if (!a.has_shared) return;
+    if (wave_id < a.n_shared_waves) {
+        switch (a.sg.bits) {
+        case 2: shared_item<2, ST>(a, wave_id, sub, cl, xr, xsum); break;
+        case 4: shared_item<4, ST>(a, wave_id, sub, cl, xr, xsum); break;
+        default: shared_item<8, ST>(a, wave_id, sub, cl, xr, xsum); break;
+        }
+        return;
+    }
+    wave_id -= a.n_shared_waves;
+    if (wave_id == 0) {
+        // shared-expert gate input [h] -> scalar (matmul(shared_gate [h,1]),
+        // execute.rs:230; weight reshaped [h] -> [h,1], loader.rs:194)
+        float v = 0.f;
+        if (sub == 0) v = lane_row_dot_any<ST>(a.sgi, 0, cl, a.h / 32, xr, xsum);
+        v = subwave_sum(v, (int)lpr);
+        if (lane == 0) a.sh_gate[0] = v;
+    }
+}
+
+// --------------------------------------------------------------- gate/up --
+template <int BITS, int ST>
+__global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeKArgs a) {
+    extern __shared__ float route_vals[];  // E floats + K ids + K weights
+    uint32_t *s_ids = reinterpret_cast<uint32_t *>(route_vals + a.E);
+    float *s_w = route_vals + a.E + a.k;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const uint32_t lpr = a.lpr_h, rpi = 64u / lpr, sub = lane / lpr, cl = lane % lpr;
+    float xr[32];
+    const float xsum = load_x_chunk(a.x, a.norm_w, a.eps, a.h, cl, (int)lpr, xr);
+    if (wv == 0) {
+        // route (sampling.metal:1-36), exact, redundantly per block
+        route_one_wave(route_vals, a.logits, a.E, a.k, (int)a.normalize, s_ids, s_w, lane);
+        if (blockIdx.x == 0 && lane == 0) {
+            for (uint32_t k = 0; k < a.k; k++) {
+                a.ids[k] = s_ids[k];
+                a.weights[k] = s_w[k];
+            }
+        }
+    }
+    __syncthreads();
+    const uint32_t wave_id = blockIdx.x * 4 + wv;
+    const uint32_t kk = wave_id / a.n_gate_waves_per_expert;
+    if (kk >= a.k) return;
+    const uint32_t item = wave_id % a.n_gate_waves_per_expert;
+    const uint32_t e = s_ids[kk];  // < E by construction of route
+    uint64_t rows[kGateFR];
+    bool ok[kGateFR];
+#pragma unroll
+    for (int f = 0; f < kGateFR; f++) {
+        const uint32_t j = (item * kGateFR + f) * rpi + sub;
+        ok[f] = j < a.ff;
+        rows[f] = (uint64_t)e * a.ff + j;
+    }
+    float g[kGateFR], u[kGateFR];
+    lane_rows_dot<BITS, ST, kGateFR>(a.gate, rows, ok, cl, a.h / 32, xr, xsum, g);
+    lane_rows_dot<BITS, ST, kGateFR>(a.up, rows, ok, cl, a.h / 32, xr, xsum, u);
+#pragma unroll
+    for (int f = 0; f < kGateFR; f++) {
+        const float gv = subwave_sum(g[f], (int)lpr), uv = subwave_sum(u[f], (int)lpr);
+        const uint32_t j = (item * kGateFR + f) * rpi + sub;
+        // activation (elementwise.metal:8-17)
+        if (ok[f] && cl == 0) a.act[(uint64_t)kk * a.ff + j] = gv / (1.0f + expf(-gv)) * uv;
+    }
+}
+
+// ------------------------------------------------------------------ down --
+// Block = 4 waves over `rows_per_block` output rows; wave w takes experts
+// w, w+4, ... of the K routed experts plus the shared one (index K), and the
+// four waves' partial sums meet in LDS.
+template <int BITS, int ST>
+__device__ __forceinline__ void down_expert(const DecodeKArgs &a, const WDesc &w, uint32_t e,
+                                            const float *act_row, uint32_t row0, uint32_t sub,
+                                            uint32_t cl, uint32_t rpi, float *part) {
+    float xr[32];
+    const float4 *src = reinterpret_cast<const float4 *>(act_row + (uint64_t)cl * 32);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 v = src[i];
+        xr[4 * i + 0] = v.x;
+        xr[4 * i + 1] = v.y;
+        xr[4 * i + 2] = v.z;
+        xr[4 * i + 3] = v.w;
+    }
+    float xsum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 32; j++) xsum += xr[j];
+    uint64_t rows[kDownFR];
+    bool ok[kDownFR];
+#pragma unroll
+    for (int f = 0; f < kDownFR; f++) {
+        const uint32_t r = row0 + f * rpi + sub;
+        ok[f] = r < a.h;
+        rows[f] = (uint64_t)e * a.h + r;
+    }
+    lane_rows_dot<BITS, ST, kDownFR>(w, rows, ok, cl, a.ff / 32, xr, xsum, part);
+}
+
+template <int BITS, int ST>
+__global__ __launch_bounds__(256) void decode_down_kernel(DecodeKArgs a) {
+    __shared__ float red_r[4][128];
+    __shared__ float red_s[4][128];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const uint32_t lpr = a.lpr_f, rpi = 64u / lpr, sub = lane / lpr, cl = lane % lpr;
+    const uint32_t rows_per_block = rpi * kDownFR;
+    const uint32_t row0 = blockIdx.x * rows_per_block;
+    float acc_r[kDownFR], acc_s[kDownFR];
+#pragma unroll
+    for (int f = 0; f < kDownFR; f++) acc_r[f] = acc_s[f] = 0.f;
+    const uint32_t n_exp = a.k + (a.has_shared ? 1u : 0u);
+    for (uint32_t kk = wv; kk < n_exp; kk += 4) {
+        float part[kDownFR];
+        if (kk < a.k) {
+            const uint32_t e = a.ids[kk];
+            down_expert<BITS, ST>(a, a.down, e, a.act + (uint64_t)kk * a.ff, row0, sub, cl, rpi,
+                                  part);
+            const float wk = a.weights[kk];
+#pragma unroll
+            for (int f = 0; f < kDownFR; f++) acc_r[f] += part[f] * wk;
+        } else {
+            switch (a.sd.bits) {
+            case 2: down_expert<2, ST>(a, a.sd, 0, a.sh_act, row0, sub, cl, rpi, part); break;
+            case 4: down_expert<4, ST>(a, a.sd, 0, a.sh_act, row0, sub, cl, rpi, part); break;
+            default: down_expert<8, ST>(a, a.sd, 0, a.sh_act, row0, sub, cl, rpi, part); break;
+            }
+#pragma unroll
+            for (int f = 0; f < kDownFR; f++) acc_s[f] += part[f];
+        }
+    }
+#pragma unroll
+    for (int f = 0; f < kDownFR; f++) {
+        const float r = subwave_sum(acc_r[f], (int)lpr), s = subwave_sum(acc_s[f], (int)lpr);
+        if (cl == 0) {
+            red_r[wv][f * rpi + sub] = r;
+            red_s[wv][f * rpi + sub] = s;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < rows_per_block) {
+        const uint32_t i = threadIdx.x, row = row0 + i;
+        if (row < a.h) {
+            // mix (elementwise.metal:47-57), then shared / (1+exp(-g)) and add
+            // (gate_scalar + add, execute.rs:231-232), then the residual
+            // (execute.rs:236)
+            float v = red_r[0][i] + red_r[1][i] + red_r[2][i] + red_r[3][i];
+            if (a.has_shared) {
+                const float sv = red_s[0][i] + red_s[1][i] + red_s[2][i] + red_s[3][i];
+                v = v + sv / (1.0f + expf(-a.sh_gate[0]));
+            }
+            if (a.resid) v = a.resid[row] + v;
+            a.out[row] = v;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ host --
+static bool pow2_chunks(uint32_t n) {
+    if (n % 32) return false;
+    const uint32_t c = n / 32;
+    return c >= 1 && c <= 64 && (c & (c - 1)) == 0;
+}
+static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+bool decode_supported(const DecodeArgs &a) {
+    const WDesc &g = a.gate;
+    if (g.bits == 0 || a.up.bits != g.bits || a.down.bits != g.bits) return false;
+    if (a.up.type != g.type || a.down.type != g.type) return false;
+    const uint32_t st = g.type;
+    if (!pow2_chunks(g.in) || !pow2_chunks(g.out)) return false;
+    if (a.router.bits && a.router.type != st) return false;
+    if (a.router.out > 4096 || a.k == 0 || a.k > 64 || a.k > a.router.out) return false;
+    if (a.has_shared) {
+        if (a.sg.bits == 0 || a.su.bits != a.sg.bits || a.sd.bits != a.sg.bits) return false;
+        if (a.sg.type != st || a.su.type != st || a.sd.type != st) return false;
+        if (a.sg.out != g.out) return false;  // shared ff == routed ff (same down layout)
+        if (a.sgi.bits && a.sgi.type != st) return false;
+    }
+    const WDesc *all[] = {&a.router, &a.gate, &a.up, &a.down, &a.sg, &a.su, &a.sd, &a.sgi};
+    const int n = a.has_shared ? 8 : 4;
+    for (int i = 0; i < n; i++)
+        if (!aligned16(all[i]->data)) return false;
+    if (!aligned16(a.x) || !aligned16(a.act) || !aligned16(a.sh_act)) return false;
+    if (a.norm_w && !aligned16(a.norm_w)) return false;
+    return true;
+}
+
+template <int BITS, int ST>
+static hipError_t launch_decode_t(Prof *p, hipStream_t s, const DecodeKArgs &k) {
+    const uint32_t pre_waves = k.n_router_waves + (k.has_shared ? k.n_shared_waves + 1 : 0);
+    prof_begin(p, s, "decode_pre");
+    hipLaunchKernelGGL((decode_pre_kernel<ST>), dim3((pre_waves + 3) / 4), dim3(256), 0, s, k);
+    hipError_t e = hipGetLastError();
+    prof_end(p, s);
+    if (e != hipSuccess) return e;
+    const uint32_t gate_waves = k.k * k.n_gate_waves_per_expert;
+    const size_t lds = (size_t)(k.E + 2 * k.k) * sizeof(float);
+    prof_begin(p, s, "decode_gateup");
+    hipLaunchKernelGGL((decode_gateup_kernel<BITS, ST>), dim3((gate_waves + 3) / 4), dim3(256), lds,
+                       s, k);
+    e = hipGetLastError();
+    prof_end(p, s);
+    if (e != hipSuccess) return e;
+    const uint32_t rows_per_block = (64u / k.lpr_f) * kDownFR;
+    prof_begin(p, s, "decode_down");
+    hipLaunchKernelGGL((decode_down_kernel<BITS, ST>), dim3((k.h + rows_per_block - 1) / rows_per_block),
+                       dim3(256), 0, s, k);
+    e = hipGetLastError();
+    prof_end(p, s);
+    return e;
+}
+
+hipError_t launch_decode(Prof *p, hipStream_t s, const DecodeArgs &a) {
+    DecodeKArgs k{};
+    k.router = a.router; k.gate = a.gate; k.up = a.up; k.down = a.down;
+    k.sg = a.sg; k.su = a.su; k.sd = a.sd; k.sgi = a.sgi;
+    k.has_shared = a.has_shared; k.k = a.k; k.normalize = a.normalize;
+    k.h = a.gate.in; k.ff = a.gate.out; k.ffs = a.has_shared ? a.sg.out : 0; k.E = a.router.out;
+    k.lpr_h = k.h / 32; k.lpr_f = k.ff / 32;
+    const uint32_t rpi_h = 64u / k.lpr_h;
+    k.n_router_waves = (k.E + rpi_h - 1) / rpi_h;
+    k.n_shared_waves = (k.ffs + rpi_h * kSharedFR - 1) / (rpi_h * kSharedFR);
+    k.n_gate_waves_per_expert = (k.ff + rpi_h * kGateFR - 1) / (rpi_h * kGateFR);
+    k.x = a.x; k.norm_w = a.norm_w; k.eps = a.eps; k.logit_bias = a.logit_bias; k.resid = a.resid;
+    k.out = a.out; k.logits = a.logits; k.ids = a.ids; k.weights = a.weights; k.act = a.act;
+    k.sh_act = a.sh_act; k.sh_gate = a.sh_gate;
+    const uint32_t st = a.gate.type;
+#define DEC_CASE(B, T) if (a.gate.bits == B && st == T) return launch_decode_t<B, T>(p, s, k);
+    DEC_CASE(2, 0) DEC_CASE(2, 1) DEC_CASE(2, 30)
+    DEC_CASE(4, 0) DEC_CASE(4, 1) DEC_CASE(4, 30)
+    DEC_CASE(8, 0) DEC_CASE(8, 1) DEC_CASE(8, 30)
+#undef DEC_CASE
+    return hipErrorInvalidValue;
+}
+
+}  // namespace moehip

@@ -1,0 +1,141 @@
+// Routing (Batch::route, crates/metal-backend/src/apple/ops/sampling.rs:21-44)
+// and token -> expert dispatch (counts, exclusive scan, stable permutation).
+#include "route.hpp"
+
+namespace moehip {
+
+// One wave per token; each wave keeps a private LDS copy of its logits row.
+__global__ __launch_bounds__(64) void route_kernel(const float *__restrict__ logits, uint32_t E,
+                                                   uint32_t K, int normalize,
+                                                   uint32_t *__restrict__ ids,
+                                                   float *__restrict__ weights) {
+    extern __shared__ float vals[];
+    const uint32_t t = blockIdx.x;
+    route_one_wave(vals, logits + (uint64_t)t * E, E, K, normalize, ids + (uint64_t)t * K,
+                   weights + (uint64_t)t * K, threadIdx.x);
+}
+
+hipError_t launch_route(Prof *p, hipStream_t s, const float *logits, uint32_t experts, uint32_t k,
+                        int normalize, uint32_t tokens, uint32_t *ids, float *weights) {
+    prof_begin(p, s, "route");
+    hipLaunchKernelGGL(route_kernel, dim3(tokens), dim3(64), experts * sizeof(float), s, logits,
+                       experts, k, normalize, ids, weights);
+    hipError_t e = hipGetLastError();
+    prof_end(p, s);
+    return e;
+}
+
+// ---------------------------------------------------------------- dispatch --
+// Pass 1: per-expert counts.  LDS histogram per block, then one global
+// atomic per touched expert; the totals are independent of atomic order.
+constexpr int kDispThreads = 256;
+constexpr int kDispItems = 8;
+
+__global__ __launch_bounds__(kDispThreads) void zero_u32_kernel(uint32_t *p, uint32_t n) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+__global__ __launch_bounds__(kDispThreads) void dispatch_count_kernel(
+    const uint32_t *__restrict__ ids, uint32_t pairs, uint32_t E, uint32_t *__restrict__ counts) {
+    extern __shared__ uint32_t hist[];
+    for (uint32_t e = threadIdx.x; e < E; e += kDispThreads) hist[e] = 0u;
+    __syncthreads();
+    const uint32_t base = blockIdx.x * kDispThreads * kDispItems;
+    for (int i = 0; i < kDispItems; i++) {
+        const uint32_t p = base + i * kDispThreads + threadIdx.x;
+        if (p < pairs) {
+            const uint32_t e = ids[p];
+            if (e < E) atomicAdd(&hist[e], 1u);
+        }
+    }
+    __syncthreads();
+    for (uint32_t e = threadIdx.x; e < E; e += kDispThreads)
+        if (hist[e]) atomicAdd(&counts[e], hist[e]);
+}
+
+// Pass 2: one block per expert.  The block sums counts[0..e) for its offset,
+// then scans all pairs in ascending order and compacts those routed to e with
+// a block-wide exclusive scan, so perm is ordered by (expert, token, k) with
+// no dependence on scheduling.
+__global__ __launch_bounds__(kDispThreads) void dispatch_place_kernel(
+    const uint32_t *__restrict__ ids, uint32_t pairs, uint32_t E,
+    const uint32_t *__restrict__ counts, uint32_t *__restrict__ offsets,
+    uint32_t *__restrict__ perm, uint32_t *__restrict__ pos) {
+    __shared__ uint32_t wsum[kDispThreads / 64];
+    __shared__ uint32_t total;
+    const uint32_t e = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    // offset of expert e
+    uint32_t part = 0;
+    for (uint32_t i = tid; i < e; i += kDispThreads) part += counts[i];
+    for (int o = 32; o >= 1; o >>= 1) part += __shfl_xor(part, o, 64);
+    if (lane == 0) wsum[wv] = part;
+    __syncthreads();
+    const uint32_t off = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    const uint32_t cnt = counts[e];
+    if (tid == 0) {
+        offsets[e] = off;
+        if (e == E - 1) offsets[E] = off + cnt;
+    }
+    __syncthreads();
+    if (cnt == 0) return;
+    uint32_t running = 0;
+    for (uint32_t base = 0; base < pairs && running < cnt; base += kDispThreads * kDispItems) {
+        // each thread owns kDispItems consecutive pairs
+        const uint32_t p0 = base + tid * kDispItems;
+        uint32_t mine = 0, mask = 0;
+#pragma unroll
+        for (int i = 0; i < kDispItems; i++) {
+            const uint32_t p = p0 + i;
+            if (p < pairs && ids[p] == e) {
+                mask |= 1u << i;
+                mine++;
+            }
+        }
+        // block exclusive scan of `mine`
+        uint32_t incl = mine;
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t v = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += v;
+        }
+        if (lane == 63) wsum[wv] = incl;
+        __syncthreads();
+        uint32_t before = 0;
+        for (int w = 0; w < wv; w++) before += wsum[w];
+        const uint32_t excl = running + before + incl - mine;
+        if (tid == 0) total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+        uint32_t at = off + excl;
+#pragma unroll
+        for (int i = 0; i < kDispItems; i++) {
+            if (mask & (1u << i)) {
+                perm[at] = p0 + i;
+                pos[p0 + i] = at;
+                at++;
+            }
+        }
+        __syncthreads();
+        running += total;
+        __syncthreads();
+    }
+}
+
+hipError_t launch_dispatch(Prof *p, hipStream_t s, const uint32_t *ids, uint32_t pairs,
+                           uint32_t experts, uint32_t *counts, uint32_t *offsets, uint32_t *perm,
+                           uint32_t *pos) {
+    prof_begin(p, s, "dispatch");
+    const uint32_t zb = (experts + kDispThreads - 1) / kDispThreads;
+    hipLaunchKernelGGL(zero_u32_kernel, dim3(zb), dim3(kDispThreads), 0, s, counts, experts);
+    const uint32_t per_block = kDispThreads * kDispItems;
+    const uint32_t nb = (pairs + per_block - 1) / per_block;
+    if (nb)
+        hipLaunchKernelGGL(dispatch_count_kernel, dim3(nb), dim3(kDispThreads),
+                           experts * sizeof(uint32_t), s, ids, pairs, experts, counts);
+    hipLaunchKernelGGL(dispatch_place_kernel, dim3(experts), dim3(kDispThreads), 0, s, ids, pairs,
+                       experts, counts, offsets, perm, pos);
+    hipError_t e = hipGetLastError();
+    prof_end(p, s);
+    return e;
+}
+
+}  // namespace moehip

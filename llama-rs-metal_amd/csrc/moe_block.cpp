@@ -1,0 +1,378 @@
+// moe_block: one MoE block over T tokens behind the C ABI, plus profiling and
+// graph capture.  The composition follows crates/model-runtime/src/execute.rs:200-236
+// (router -> route -> gate/up -> swiglu -> down -> mix -> shared expert ->
+// sigmoid gate -> add -> residual), with three interchangeable executions:
+//   MOE_PATH_OPS      the reference's own per-token op sequence (14 ops per token)
+//   MOE_PATH_GROUPED  token-batched: route all tokens, dispatch by expert,
+//                     grouped expert products, one combine
+//   MOE_PATH_AUTO     fused 3-kernel decode for one token, grouped otherwise
+#include "abi_common.hpp"
+
+namespace {
+
+struct WsLayout {
+    uint64_t logits, ids, weights, counts, offsets, perm, pos, act, yexp, sh_act, sh_up, sh_gate,
+        sh_out, xnorm, gates, ups, eo, proj, sgv, total;
+};
+
+inline uint64_t al64(uint64_t n) { return (n + 63) & ~63ull; }
+
+WsLayout ws_layout(uint64_t T, uint64_t E, uint64_t K, uint64_t h, uint64_t ff, uint64_t ffs) {
+    WsLayout L{};
+    uint64_t o = 0;
+    auto take = [&](uint64_t &field, uint64_t n) {
+        field = o;
+        o += al64(n ? n : 1);
+    };
+    take(L.logits, T * E);
+    take(L.ids, T * K);
+    take(L.weights, T * K);
+    take(L.counts, E);
+    take(L.offsets, E + 1);
+    take(L.perm, T * K);
+    take(L.pos, T * K);
+    take(L.act, T * K * ff);
+    take(L.yexp, T * K * h);
+    take(L.sh_act, T * ffs);
+    take(L.sh_up, T * ffs);
+    take(L.sh_gate, T);
+    take(L.sh_out, T * h);
+    take(L.xnorm, T * h);
+    take(L.gates, K * ff);
+    take(L.ups, K * ff);
+    take(L.eo, K * h);
+    take(L.proj, h);
+    take(L.sgv, 1);
+    L.total = o;
+    return L;
+}
+
+struct Dims {
+    uint64_t h, ff, E, K, ffs;
+};
+
+// Shape contract of the MoE binding (crates/model-runtime/src/loader.rs:172-203).
+moe_status check_block(moe_gpu *g, const moe_block_weights *w, Dims &d) {
+    if (!w) return shape(g, "missing block weights");
+    moe_status st;
+    if ((st = check_weight(g, &w->router, "router")) || (st = check_weight(g, &w->gate, "expert gates")) ||
+        (st = check_weight(g, &w->up, "expert ups")) || (st = check_weight(g, &w->down, "expert downs")))
+        return st;
+    const moe_weight &r = w->router, &ga = w->gate, &u = w->up, &dn = w->down;
+    if (r.ndims != 2 || ga.ndims != 3 || u.ndims != 3 || dn.ndims != 3)
+        return shape(g, "MoE routing dimensions");
+    d.h = r.dims[0];
+    d.E = r.dims[1];
+    d.K = w->experts_used;
+    if (d.K == 0 || d.K > d.E) return shape(g, "MoE routing dimensions");
+    if (ga.dims[0] != d.h || ga.dims[2] != d.E) return shape(g, "expert gates dimensions");
+    d.ff = ga.dims[1];
+    if (u.dims[0] != d.h || u.dims[1] != d.ff || u.dims[2] != d.E) return shape(g, "expert ups dimensions");
+    if (dn.dims[0] != d.ff || dn.dims[1] != d.h || dn.dims[2] != d.E)
+        return shape(g, "expert downs dimensions");
+    d.ffs = 0;
+    if (w->has_shared) {
+        if ((st = check_weight(g, &w->shared_gate, "shared gate")) ||
+            (st = check_weight(g, &w->shared_up, "shared up")) ||
+            (st = check_weight(g, &w->shared_down, "shared down")) ||
+            (st = check_weight(g, &w->shared_gate_inp, "shared expert gate")))
+            return st;
+        const moe_weight &sg = w->shared_gate, &su = w->shared_up, &sd = w->shared_down,
+                         &gi = w->shared_gate_inp;
+        if (sg.ndims != 2 || sg.dims[0] != d.h) return shape(g, "shared gate dimensions");
+        d.ffs = sg.dims[1];
+        if (su.ndims != 2 || su.dims[0] != d.h || su.dims[1] != d.ffs) return shape(g, "shared up dimensions");
+        if (sd.ndims != 2 || sd.dims[0] != d.ffs || sd.dims[1] != d.h)
+            return shape(g, "shared down dimensions");
+        if (gi.dims[0] != d.h || (gi.ndims == 2 && gi.dims[1] != 1) || gi.ndims > 2)
+            return shape(g, "shared expert gate dimensions");
+    }
+    if (d.E > 16384) return shape(g, "more than 16384 experts");
+    return MOE_OK;
+}
+
+float *fp(const moe_buffer &b, uint64_t off = 0) { return static_cast<float *>(b.ptr) + off; }
+uint32_t *up32(const moe_buffer &b, uint64_t off = 0) { return static_cast<uint32_t *>(b.ptr) + off; }
+bool has(const moe_buffer &b) { return b.ptr != nullptr && b.len != 0; }
+
+WDesc gate_inp_desc(const moe_weight &w) {
+    WDesc d = wdesc(w);
+    d.out = 1;  // [h] reshaped [h, 1] (loader.rs:194)
+    d.experts = 1;
+    return d;
+}
+
+#define TRY(expr)                                       \
+    do {                                                \
+        hipError_t e_ = (expr);                         \
+        if (e_ != hipSuccess) return gpu_err(g, e_, #expr); \
+    } while (0)
+
+// The reference's per-token op sequence (execute.rs:208-233 and encode_dense :251-267).
+moe_status run_ops(moe_gpu *g, const moe_block_weights *w, const Dims &d, const float *xin,
+                   const float *xres, float *out, uint64_t T, const moe_block_io *io,
+                   const WsLayout &L, float *ws, float *logits, uint32_t *ids, float *wts) {
+    Prof *p = &g->prof;
+    hipStream_t s = g->stream;
+    const WDesc R = wdesc(w->router), G = wdesc(w->gate), U = wdesc(w->up), D = wdesc(w->down);
+    const uint32_t K = (uint32_t)d.K;
+    float *gates = ws + L.gates, *ups = ws + L.ups, *eo = ws + L.eo, *proj = ws + L.proj;
+    for (uint64_t t = 0; t < T; t++) {
+        const float *xt = xin + t * d.h;
+        float *lt = logits + t * d.E;
+        uint32_t *it = ids + t * K;
+        float *wt = wts + t * K;
+        TRY(launch_gemv(p, s, R, xt, 0, nullptr, 1, lt, 1));
+        if (has(io->logit_bias)) TRY(launch_add(p, s, lt, fp(io->logit_bias, t * d.E), lt, d.E));
+        TRY(launch_route(p, s, lt, (uint32_t)d.E, K, w->normalize ? 1 : 0, 1, it, wt));
+        TRY(launch_gemv(p, s, G, xt, 0, it, K, gates, 1));
+        TRY(launch_gemv(p, s, U, xt, 0, it, K, ups, 1));
+        TRY(launch_swiglu(p, s, gates, ups, gates, K * d.ff));
+        TRY(launch_gemv(p, s, D, gates, d.ff, it, K, eo, 1));
+        TRY(launch_mix(p, s, eo, wt, K, d.h, proj));
+        if (w->has_shared) {
+            float *sg = ws + L.sh_act, *su = ws + L.sh_up, *so = ws + L.sh_out, *sgv = ws + L.sgv;
+            TRY(launch_gemv(p, s, wdesc(w->shared_gate), xt, 0, nullptr, 1, sg, 1));
+            TRY(launch_gemv(p, s, wdesc(w->shared_up), xt, 0, nullptr, 1, su, 1));
+            TRY(launch_swiglu(p, s, sg, su, sg, d.ffs));
+            TRY(launch_gemv(p, s, wdesc(w->shared_down), sg, 0, nullptr, 1, so, 1));
+            TRY(launch_gemv(p, s, gate_inp_desc(w->shared_gate_inp), xt, 0, nullptr, 1, sgv, 1));
+            TRY(launch_gate_scalar(p, s, so, sgv, so, d.h));
+            TRY(launch_add(p, s, proj, so, proj, d.h));
+        }
+        if (io->residual)
+            TRY(launch_add(p, s, xres + t * d.h, proj, out + t * d.h, d.h));
+        else
+            TRY(launch_copy(p, s, proj, out + t * d.h, d.h));
+    }
+    return MOE_OK;
+}
+
+moe_status run_grouped(moe_gpu *g, const moe_block_weights *w, const Dims &d, const float *xin,
+                       const float *xres, float *out, uint64_t T, const moe_block_io *io,
+                       const WsLayout &L, float *ws, float *logits, uint32_t *ids, float *wts) {
+    Prof *p = &g->prof;
+    hipStream_t s = g->stream;
+    const uint32_t K = (uint32_t)d.K, E = (uint32_t)d.E;
+    const WDesc G = wdesc(w->gate), U = wdesc(w->up), D = wdesc(w->down);
+    uint32_t *counts = reinterpret_cast<uint32_t *>(ws + L.counts);
+    uint32_t *offsets = reinterpret_cast<uint32_t *>(ws + L.offsets);
+    uint32_t *perm = reinterpret_cast<uint32_t *>(ws + L.perm);
+    uint32_t *pos = reinterpret_cast<uint32_t *>(ws + L.pos);
+    float *act = ws + L.act, *yexp = ws + L.yexp;
+    TRY(launch_gemv(p, s, wdesc(w->router), xin, 0, nullptr, 1, logits, (uint32_t)T));
+    if (has(io->logit_bias)) TRY(launch_add(p, s, logits, fp(io->logit_bias), logits, T * d.E));
+    TRY(launch_route(p, s, logits, E, K, w->normalize ? 1 : 0, (uint32_t)T, ids, wts));
+    TRY(launch_dispatch(p, s, ids, (uint32_t)(T * K), E, counts, offsets, perm, pos));
+    TRY(launch_grouped_gateup(p, s, G, U, xin, offsets, perm, K, E, act));
+    TRY(launch_grouped_down(p, s, D, act, offsets, E, (uint32_t)(T * K), yexp));
+    const float *so = nullptr, *sgv = nullptr;
+    if (w->has_shared) {
+        float *sg = ws + L.sh_act, *su = ws + L.sh_up, *sout = ws + L.sh_out, *sgt = ws + L.sh_gate;
+        TRY(launch_gemv(p, s, wdesc(w->shared_gate), xin, 0, nullptr, 1, sg, (uint32_t)T));
+        TRY(launch_gemv(p, s, wdesc(w->shared_up), xin, 0, nullptr, 1, su, (uint32_t)T));
+        TRY(launch_swiglu(p, s, sg, su, sg, T * d.ffs));
+        TRY(launch_gemv(p, s, wdesc(w->shared_down), sg, 0, nullptr, 1, sout, (uint32_t)T));
+        TRY(launch_gemv(p, s, gate_inp_desc(w->shared_gate_inp), xin, 0, nullptr, 1, sgt, (uint32_t)T));
+        so = sout;
+        sgv = sgt;
+    }
+    TRY(launch_combine(p, s, yexp, pos, wts, K, so, sgv, io->residual ? xres : nullptr, out,
+                       (uint32_t)T, (uint32_t)d.h));
+    return MOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+moe_status moe_block_workspace(const moe_block_weights *w, uint64_t tokens, uint64_t *elems) {
+    if (!w || !elems || tokens == 0) return MOE_ERR_SHAPE;
+    const uint64_t h = w->router.dims[0], E = w->router.dims[1], K = w->experts_used;
+    const uint64_t ff = w->gate.dims[1], ffs = w->has_shared ? w->shared_gate.dims[1] : 0;
+    *elems = ws_layout(tokens, E, K, h, ff, ffs).total;
+    return MOE_OK;
+}
+
+moe_status moe_block(moe_gpu *g, const moe_block_weights *w, moe_buffer x, moe_buffer out,
+                     uint64_t tokens, const moe_block_io *io) {
+    moe_status st = need_batch(g);
+    if (st) return st;
+    if (!io) return shape(g, "missing block io");
+    Dims d{};
+    if ((st = check_block(g, w, d))) return st;
+    if (tokens == 0 || tokens > 65535) return shape(g, "tokens must be in [1, 65535]");
+    const uint64_t T = tokens;
+    if (x.len != T * d.h || out.len != T * d.h) return shape(g, "block input/output length");
+    const WsLayout L = ws_layout(T, d.E, d.K, d.h, d.ff, d.ffs);
+    if (io->workspace.len < L.total) return shape(g, "workspace too small");
+    if (has(io->logit_bias) && io->logit_bias.len != T * d.E) return shape(g, "logit bias length");
+    if (has(io->logits_out) && io->logits_out.len != T * d.E) return shape(g, "logits output length");
+    if (has(io->ids_out) && io->ids_out.len != T * d.K) return shape(g, "ids output length");
+    if (has(io->weights_out) && io->weights_out.len != T * d.K) return shape(g, "weights output length");
+    if (has(io->norm_weight) &&
+        (io->norm_weight.len != d.h || !std::isfinite(io->norm_eps) || io->norm_eps <= 0.f))
+        return shape(g, "norm");
+    if (io->path > MOE_PATH_GROUPED) return shape(g, "unknown path");
+    // ownership
+    std::vector<Range> reads{rng(x)};
+    std::vector<Range> writes{rng(out), rng(io->workspace)};
+    if ((st = check_own(g, {rng(x), rng(out), rng(io->workspace)}))) return st;
+    const moe_buffer *opt_in[] = {&io->logit_bias, &io->norm_weight};
+    const moe_buffer *opt_out[] = {&io->logits_out, &io->ids_out, &io->weights_out};
+    for (auto b : opt_in)
+        if (has(*b)) {
+            if ((st = check_own(g, {rng(*b)}))) return st;
+            reads.push_back(rng(*b));
+        }
+    for (auto b : opt_out)
+        if (has(*b)) {
+            if ((st = check_own(g, {rng(*b)}))) return st;
+            writes.push_back(rng(*b));
+        }
+    const moe_weight *ws_list[] = {&w->router, &w->gate, &w->up, &w->down, &w->shared_gate,
+                                   &w->shared_up, &w->shared_down, &w->shared_gate_inp};
+    for (int i = 0; i < (w->has_shared ? 8 : 4); i++)
+        for (const Range &r : weight_ranges(*ws_list[i])) reads.push_back(r);
+    // out may be exactly x (in-place residual stream); everything else is disjoint
+    for (size_t i = 0; i < writes.size(); i++) {
+        for (size_t j = i + 1; j < writes.size(); j++)
+            if (overlaps(writes[i], writes[j])) return shape(g, "overlapping GPU outputs");
+        for (size_t r = 0; r < reads.size(); r++)
+            if (overlaps(writes[i], reads[r]) && !(i == 0 && r == 0 && same(writes[i], reads[r])))
+                return shape(g, "GPU input/output alias");
+    }
+
+    float *ws = fp(io->workspace);
+    float *logits = has(io->logits_out) ? fp(io->logits_out) : ws + L.logits;
+    uint32_t *ids = has(io->ids_out) ? up32(io->ids_out) : reinterpret_cast<uint32_t *>(ws + L.ids);
+    float *wts = has(io->weights_out) ? fp(io->weights_out) : ws + L.weights;
+    const float *xraw = fp(x);
+    float *o = fp(out);
+    const float *nw = has(io->norm_weight) ? fp(io->norm_weight) : nullptr;
+
+    // fused single-token decode
+    if (io->path == MOE_PATH_AUTO && T == 1) {
+        DecodeArgs a{};
+        a.router = wdesc(w->router);
+        a.gate = wdesc(w->gate);
+        a.up = wdesc(w->up);
+        a.down = wdesc(w->down);
+        a.has_shared = w->has_shared;
+        if (w->has_shared) {
+            a.sg = wdesc(w->shared_gate);
+            a.su = wdesc(w->shared_up);
+            a.sd = wdesc(w->shared_down);
+            a.sgi = gate_inp_desc(w->shared_gate_inp);
+        }
+        a.k = (uint32_t)d.K;
+        a.normalize = w->normalize ? 1 : 0;
+        a.x = xraw;
+        a.norm_w = nw;
+        a.eps = io->norm_eps;
+        a.logit_bias = has(io->logit_bias) ? fp(io->logit_bias) : nullptr;
+        a.resid = io->residual ? xraw : nullptr;
+        a.out = o;
+        a.logits = logits;
+        a.ids = ids;
+        a.weights = wts;
+        a.act = ws + L.act;
+        a.sh_act = ws + L.sh_act;
+        a.sh_gate = ws + L.sh_gate;
+        if (decode_supported(a)) return launched(g, launch_decode(&g->prof, g->stream, a), "decode");
+    }
+
+    const float *xin = xraw;
+    if (nw) {
+        float *xn = ws + L.xnorm;
+        // Batch::norm over T rows (execute.rs:197)
+        hipError_t e = launch_norm(&g->prof, g->stream, xraw, nw, MOE_F32, xn, (uint32_t)T,
+                                   (uint32_t)d.h, (uint32_t)d.h, io->norm_eps);
+        if (e != hipSuccess) return gpu_err(g, e, "norm");
+        xin = xn;
+    }
+    if (io->path == MOE_PATH_OPS)
+        return run_ops(g, w, d, xin, xraw, o, T, io, L, ws, logits, ids, wts);
+    return run_grouped(g, w, d, xin, xraw, o, T, io, L, ws, logits, ids, wts);
+}
+
+// ============================================================ profiling ==
+moe_status moe_profile_enable(moe_gpu *g, int enable) {
+    if (!g) return MOE_ERR_SHAPE;
+    g->prof.enabled = enable != 0;
+    return MOE_OK;
+}
+
+moe_status moe_profile_count(moe_gpu *g, uint32_t *n) {
+    if (!g || !n) return MOE_ERR_SHAPE;
+    (void)hipSetDevice(g->device);
+    prof_collect(&g->prof, g->stream);
+    *n = (uint32_t)g->prof.entries.size();
+    return MOE_OK;
+}
+
+moe_status moe_profile_get(moe_gpu *g, uint32_t index, char *name, size_t cap, uint64_t *launches,
+                           double *seconds) {
+    if (!g) return MOE_ERR_SHAPE;
+    (void)hipSetDevice(g->device);
+    prof_collect(&g->prof, g->stream);
+    if (index >= g->prof.entries.size()) return shape(g, "profile index");
+    const ProfEntry &e = g->prof.entries[index];
+    if (name && cap) std::snprintf(name, cap, "%s", e.name.c_str());
+    if (launches) *launches = e.launches;
+    if (seconds) *seconds = e.seconds;
+    return MOE_OK;
+}
+
+moe_status moe_profile_reset(moe_gpu *g) {
+    if (!g) return MOE_ERR_SHAPE;
+    (void)hipSetDevice(g->device);
+    prof_collect(&g->prof, g->stream);
+    g->prof.entries.clear();
+    return MOE_OK;
+}
+
+// ================================================================ graphs ==
+moe_status moe_graph_begin(moe_gpu *g) {
+    moe_status st = need_no_batch(g);
+    if (st) return st;
+    if (g->prof.enabled) return shape(g, "disable profiling before capturing a graph");
+    hipError_t e = hipStreamBeginCapture(g->stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return gpu_err(g, e, "begin capture");
+    g->in_batch = true;
+    g->capturing = true;
+    return MOE_OK;
+}
+
+moe_status moe_graph_end(moe_gpu *g, moe_graph **out) {
+    if (!g || !out) return MOE_ERR_SHAPE;
+    if (!g->capturing) return shape(g, "no graph capture in progress");
+    (void)hipSetDevice(g->device);
+    g->capturing = false;
+    g->in_batch = false;
+    moe_graph *gr = new moe_graph();
+    hipError_t e = hipStreamEndCapture(g->stream, &gr->graph);
+    if (e == hipSuccess) e = hipGraphInstantiate(&gr->exec, gr->graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        moe_graph_destroy(gr);
+        return gpu_err(g, e, "graph");
+    }
+    *out = gr;
+    return MOE_OK;
+}
+
+moe_status moe_graph_launch(moe_gpu *g, moe_graph *gr) {
+    moe_status st = need_batch(g);
+    if (st) return st;
+    if (!gr || g->capturing) return shape(g, "graph launch");
+    return launched(g, hipGraphLaunch(gr->exec, g->stream), "graph launch");
+}
+
+void moe_graph_destroy(moe_graph *gr) {
+    if (!gr) return;
+    if (gr->exec) (void)hipGraphExecDestroy(gr->exec);
+    if (gr->graph) (void)hipGraphDestroy(gr->graph);
+    delete gr;
+}
+
+}  // extern "C"

@@ -1,0 +1,113 @@
+// Internal interfaces between the C ABI (moe_abi.cpp) and the kernel files.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace moehip {
+
+// Kernel-side view of one weight tensor (dims [in, out, experts]).
+// bits == 0: dense elements of `type` (0 F32, 1 F16, 30 BF16).
+// bits in {2,4,8}: packed u32 codes; `type` is the scale/bias dtype.
+struct WDesc {
+    const void *data;
+    const void *scales;
+    const void *biases;
+    uint32_t bits;
+    uint32_t type;
+    uint32_t in;
+    uint32_t out;
+    uint32_t experts;
+    uint32_t gshift;  // log2(group_size); 0 for dense
+};
+
+// Launch-side profiling hook: every launcher brackets its kernel with
+// prof_begin/prof_end (no-ops unless profiling is enabled on the gpu).
+struct Prof;
+void prof_begin(Prof *p, hipStream_t s, const char *name);
+void prof_end(Prof *p, hipStream_t s);
+
+// Work buffers of the fused/grouped MoE block (all device pointers).
+struct BlockBufs {
+    float *logits;    // [T, E]
+    uint32_t *ids;    // [T, K]
+    float *weights;   // [T, K]
+    uint32_t *counts; // [E]
+    uint32_t *offsets;// [E+1]
+    uint32_t *perm;   // [T*K]
+    uint32_t *pos;    // [T*K]
+    float *act;       // [T*K, ff]  (F32 SwiGLU outputs in perm order)
+    float *yexp;      // [T*K, h]   expert outputs in perm order (grouped path)
+    float *sh_act;    // [T, ffs]
+    float *sh_gate;   // [T]
+    float *sh_out;    // [T, h]
+    float *xnorm;     // [T, h] RMSNorm'ed input (when a norm weight is given)
+    uint16_t *xb16;   // [T, h] bf16 copy of the block input (MFMA path)
+    uint16_t *act16;  // [T*K, ff] bf16 SwiGLU outputs (MFMA path)
+    uint32_t *tiles;  // MFMA tile schedule
+};
+
+// ---- generic products (k_gemv.hip) ----
+// y[(sel*tokens + t)*out + r] = W_expert(sel) row r . x_sel_t
+//   matmul:        nsel = 1, ids = nullptr, x_sel_stride = 0
+//   expert_matmul: nsel = nids, tokens = 1, x_sel_stride = per_expert ? in : 0
+hipError_t launch_gemv(Prof *p, hipStream_t s, const WDesc &w, const float *x,
+                       uint64_t x_sel_stride, const uint32_t *ids, uint32_t nsel, float *y,
+                       uint32_t tokens);
+
+// ---- routing + dispatch (k_route.hip) ----
+hipError_t launch_route(Prof *p, hipStream_t s, const float *logits, uint32_t experts, uint32_t k,
+                        int normalize, uint32_t tokens, uint32_t *ids, float *weights);
+hipError_t launch_dispatch(Prof *p, hipStream_t s, const uint32_t *ids, uint32_t pairs,
+                           uint32_t experts, uint32_t *counts, uint32_t *offsets, uint32_t *perm,
+                           uint32_t *pos);
+
+// ---- element-wise (k_elem.hip) ----
+hipError_t launch_swiglu(Prof *p, hipStream_t s, const float *a, const float *b, float *y,
+                         uint64_t n);
+hipError_t launch_mix(Prof *p, hipStream_t s, const float *x, const float *w, uint32_t k,
+                      uint64_t n, float *y);
+hipError_t launch_gate_scalar(Prof *p, hipStream_t s, const float *x, const float *g, float *y,
+                              uint64_t n);
+hipError_t launch_add(Prof *p, hipStream_t s, const float *a, const float *b, float *y,
+                      uint64_t n);
+hipError_t launch_norm(Prof *p, hipStream_t s, const float *x, const void *w, uint32_t wtype,
+                       float *y, uint32_t heads, uint32_t n, uint32_t stride, float eps);
+hipError_t launch_copy(Prof *p, hipStream_t s, const float *src, float *dst, uint64_t n);
+// out[t, i] = sum_k w[t,k] * yexp[pos[t*K+k], i] (+ sigmoid(sh_gate[t]) * sh_out[t, i])
+//             (+ resid[t, i])
+hipError_t launch_combine(Prof *p, hipStream_t s, const float *yexp, const uint32_t *pos,
+                          const float *w, uint32_t k, const float *sh_out, const float *sh_gate,
+                          const float *resid, float *out, uint32_t tokens, uint32_t h);
+
+// ---- grouped expert products on VALU (k_grouped.hip) ----
+// act[p, j] = silu(x_t . G_e[j]) * (x_t . U_e[j]) for every dispatched pair p
+// (perm order), t = perm[p] / K, e = expert of the segment holding p.
+hipError_t launch_grouped_gateup(Prof *p, hipStream_t s, const WDesc &gate, const WDesc &up,
+                                 const float *x, const uint32_t *offsets, const uint32_t *perm,
+                                 uint32_t k, uint32_t experts, float *act);
+// yexp[p, r] = D_e[r] . act[p]
+hipError_t launch_grouped_down(Prof *p, hipStream_t s, const WDesc &down, const float *act,
+                               const uint32_t *offsets, uint32_t experts, uint32_t pairs,
+                               float *yexp);
+
+// ---- fused single-token decode (k_decode.hip) ----
+struct DecodeArgs {
+    WDesc router, gate, up, down, sg, su, sd, sgi;
+    uint32_t has_shared, k, normalize;
+    const float *x;          // [h] block input
+    const float *norm_w;     // [h] RMSNorm weight or nullptr
+    float eps;
+    const float *logit_bias; // [E] or nullptr
+    const float *resid;      // [h] or nullptr
+    float *out;              // [h]
+    float *logits;           // [E]
+    uint32_t *ids;           // [K]
+    float *weights;          // [K]
+    float *act;              // [K, ff]
+    float *sh_act;           // [ffs]
+    float *sh_gate;          // [1]
+};
+bool decode_supported(const DecodeArgs &a);
+hipError_t launch_decode(Prof *p, hipStream_t s, const DecodeArgs &a);
+
+}  // namespace moehip

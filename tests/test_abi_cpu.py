@@ -1,0 +1,87 @@
+"""The C ABI library on the CPU: it loads, exports every symbol the header
+declares, the Python mirror binds exactly those, and the pure-host entry
+points behave (no GPU compute here)."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+from hip_backend import api
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                      "moe_hip.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(moe_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_header_declares_the_op_surface():
+    names = declared()
+    for op in ["moe_matmul", "moe_expert_matmul", "moe_route", "moe_swiglu", "moe_mix",
+               "moe_gate_scalar", "moe_add", "moe_norm", "moe_batch_begin", "moe_batch_finish",
+               "moe_block", "moe_dispatch", "moe_route_tokens"]:
+        assert op in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = C.CDLL(api.LIB_PATH)
+    missing = [n for n in declared() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_python_mirror_binds_exactly_the_header():
+    assert sorted(api.SIGNATURES) == declared()
+    api.load_library()
+
+
+def test_version_and_view_are_host_only():
+    lib = api.load_library()
+    assert b"gfx950" in lib.moe_version()
+    b = api.MoeBufferC(C.c_void_p(4096), 10)
+    out = api.MoeBufferC()
+    assert lib.moe_view(b, 2, 8, C.byref(out)) == 0
+    assert out.ptr == 4096 + 8 and out.len == 8
+    assert lib.moe_view(b, 3, 8, C.byref(out)) == 3          # view bounds (apple.rs:57-59)
+    assert lib.moe_view(b, 0, 0, C.byref(out)) == 3          # empty view
+    assert lib.moe_view(b, 2 ** 64 - 1, 2, C.byref(out)) == 3  # overflow
+
+
+def test_workspace_size_is_host_only():
+    lib = api.load_library()
+    w = api.MoeBlockWeightsC()
+    w.router.ndims, w.router.dims[0], w.router.dims[1] = 2, 2048, 512
+    w.gate.ndims = 3
+    w.gate.dims[0], w.gate.dims[1], w.gate.dims[2] = 2048, 512, 512
+    w.has_shared = 1
+    w.shared_gate.dims[1] = 512
+    w.experts_used = 10
+    n = C.c_uint64()
+    assert lib.moe_block_workspace(C.byref(w), 1, C.byref(n)) == 0
+    # logits + ids + weights + counts + offsets + perm + pos + act + yexp + shared ... > minimum
+    assert n.value >= 512 + 10 * 512 + 10 * 2048
+    assert lib.moe_block_workspace(C.byref(w), 0, C.byref(n)) == 3
+
+
+def test_gpu_create_without_device_is_unavailable():
+    # On a machine with no gfx950 device the library refuses with
+    # Error::Unavailable; it never falls back to the CPU.
+    lib = api.load_library()
+    h = C.c_void_p()
+    st = lib.moe_gpu_create(0, C.byref(h))
+    if st == 0:
+        lib.moe_gpu_destroy(h)
+        pytest.skip("a gfx950 device is present")
+    assert st == 1
+    with pytest.raises(api.UnavailableError):
+        api.Gpu()
+
+
+def test_null_handles_are_rejected():
+    lib = api.load_library()
+    assert lib.moe_batch_begin(None) == 3
+    assert lib.moe_profile_enable(None, 1) == 3
+    assert lib.moe_allocated_bytes(None) == 0
