@@ -29,22 +29,98 @@ __device__ __forceinline__ float load_scalar(const void *p, uint64_t i) {
     }
 }
 
-// Sum over the 64 lanes of a wave (butterfly; every lane gets the total).
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
+// ---- cross-lane reductions: DPP within 16-lane rows, gfx950 permlane swaps
+// across rows (no LDS round trips, no SGPR round trips).  All lanes of the
+// wave must be active.  dpp_ctrl codes (gfx9 DPP): quad_perm [1,0,3,2],
+// quad_perm [2,3,0,1], row_half_mirror, row_mirror, row_ror:4, row_ror:8.
+constexpr int kDppQuad1 = 0xB1;
+constexpr int kDppQuad2 = 0x4E;
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+constexpr int kDppRor4 = 0x124;
+constexpr int kDppRor8 = 0x128;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
 }
-// Sum over aligned groups of `width` lanes (width a power of two <= 64).
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);
+}
+__device__ __forceinline__ float readlane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ uint32_t readlane_u(uint32_t v, int l) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, l);
+}
+// v[l] op v[l ^ 16] and v[l] op v[l ^ 32] (v_permlane16/32_swap: each returns
+// the value and its partner across the row / half-wave boundary).
+__device__ __forceinline__ float add_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false);
+    return __int_as_float(r[0]) + __int_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+    return __int_as_float(r[0]) + __int_as_float(r[1]);
+}
+__device__ __forceinline__ uint32_t max_xor16_u(uint32_t v) {
+    const auto r = __builtin_amdgcn_permlane16_swap((int)v, (int)v, false, false);
+    return max((uint32_t)r[0], (uint32_t)r[1]);
+}
+__device__ __forceinline__ uint32_t max_xor32_u(uint32_t v) {
+    const auto r = __builtin_amdgcn_permlane32_swap((int)v, (int)v, false, false);
+    return max((uint32_t)r[0], (uint32_t)r[1]);
+}
+__device__ __forceinline__ uint32_t min_xor16_u(uint32_t v) {
+    const auto r = __builtin_amdgcn_permlane16_swap((int)v, (int)v, false, false);
+    return min((uint32_t)r[0], (uint32_t)r[1]);
+}
+__device__ __forceinline__ uint32_t min_xor32_u(uint32_t v) {
+    const auto r = __builtin_amdgcn_permlane32_swap((int)v, (int)v, false, false);
+    return min((uint32_t)r[0], (uint32_t)r[1]);
+}
+
+// Sum over aligned groups of `width` lanes (a power of two <= 64, uniform);
+// every lane of a group receives its group's sum.  After each step the
+// partial is uniform inside the group reduced so far, so the mirrors pair
+// each lane with the other half.
 __device__ __forceinline__ float subwave_sum(float v, int width) {
-    for (int o = width >> 1; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+    if (width >= 2) v += dpp_f<kDppQuad1>(v);
+    if (width >= 4) v += dpp_f<kDppQuad2>(v);
+    if (width >= 8) v += dpp_f<kDppHalfMirror>(v);
+    if (width >= 16) v += dpp_f<kDppMirror>(v);
+    if (width >= 32) v = add_xor16(v);
+    if (width >= 64) v = add_xor32(v);
     return v;
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-    return v;
+// Wave sum, identical in every lane (lane 0's association order).
+__device__ __forceinline__ float wave_sum(float v) { return readlane_f(subwave_sum(v, kWave), 0); }
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, dpp_u<kDppQuad1>(v));
+    v = max(v, dpp_u<kDppQuad2>(v));
+    v = max(v, dpp_u<kDppHalfMirror>(v));
+    v = max(v, dpp_u<kDppMirror>(v));
+    return max_xor32_u(max_xor16_u(v));
 }
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+    v = min(v, dpp_u<kDppQuad1>(v));
+    v = min(v, dpp_u<kDppQuad2>(v));
+    v = min(v, dpp_u<kDppHalfMirror>(v));
+    v = min(v, dpp_u<kDppMirror>(v));
+    return min_xor32_u(min_xor16_u(v));
+}
+// Order-preserving key of a non-NaN float (unsigned compare = float compare;
+// -0 is folded onto +0 so the two still tie, as under float `>`).
+__device__ __forceinline__ uint32_t fkey(float f) {
+    const uint32_t b = __float_as_uint(f + 0.0f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float funkey(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+// Max over the wave of non-NaN floats (NaN inputs must be pre-filtered).
+__device__ __forceinline__ float wave_max(float v) { return funkey(wave_max_u32(fkey(v))); }
 
 // Byte N of a word as float (selects to v_cvt_f32_ubyteN).
 template <int N>

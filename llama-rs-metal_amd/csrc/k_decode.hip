@@ -171,11 +171,93 @@ struct DecodeKArgs {
     float *weights, *act, *sh_act, *sh_gate;
 };
 
-constexpr int kSharedFR = 2;  // shared ff indices per sub-wave in decode_pre
 constexpr int kGateFR = 4;    // routed ff indices per sub-wave in decode_gateup
+
+// Reduce-scatter of four (gate, up) partial pairs over an lpr-lane sub-wave
+// (lpr >= 16): two exchange steps halve the set per step (xor 1, xor 2 via
+// quad_perm), then the remaining pair is summed over the lanes sharing
+// lane & 3 (row_ror 4 and 8, then permlane xor 16 / 32).  Lane cl < 4 of the
+// sub-wave ends with the sums of pair f = 2*(cl & 1) + ((cl >> 1) & 1).
+__device__ __forceinline__ int rs4_index(uint32_t cl) { return 2 * (cl & 1) + ((cl >> 1) & 1); }
+__device__ __forceinline__ void rs4_pairs(const float *g, const float *u, int lane, uint32_t lpr,
+                                          float &go, float &uo) {
+    const bool b0 = lane & 1, b1 = (lane >> 1) & 1;
+    float g2[2], u2[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const float sg = b0 ? g[i] : g[i + 2], kg = b0 ? g[i + 2] : g[i];
+        const float su = b0 ? u[i] : u[i + 2], ku = b0 ? u[i + 2] : u[i];
+        g2[i] = kg + dpp_f<kDppQuad1>(sg);
+        u2[i] = ku + dpp_f<kDppQuad1>(su);
+    }
+    const float sg = b1 ? g2[0] : g2[1], kg = b1 ? g2[1] : g2[0];
+    const float su = b1 ? u2[0] : u2[1], ku = b1 ? u2[1] : u2[0];
+    go = kg + dpp_f<kDppQuad2>(sg);
+    uo = ku + dpp_f<kDppQuad2>(su);
+    go += dpp_f<kDppRor4>(go);
+    uo += dpp_f<kDppRor4>(uo);
+    go += dpp_f<kDppRor8>(go);
+    uo += dpp_f<kDppRor8>(uo);
+    if (lpr >= 32) {
+        go = add_xor16(go);
+        uo = add_xor16(uo);
+    }
+    if (lpr >= 64) {
+        go = add_xor32(go);
+        uo = add_xor32(uo);
+    }
+}
+
+// Reduce-scatter of two (routed, shared) partial pairs over an lpr-lane
+// sub-wave (lpr >= 16): lane cl < 2 ends with pair f = cl & 1.
+__device__ __forceinline__ void rs2_pairs(const float *r, const float *sh, int lane, uint32_t lpr,
+                                          float &ro, float &so) {
+    const bool b0 = lane & 1;
+    ro = (b0 ? r[1] : r[0]) + dpp_f<kDppQuad1>(b0 ? r[0] : r[1]);
+    so = (b0 ? sh[1] : sh[0]) + dpp_f<kDppQuad1>(b0 ? sh[0] : sh[1]);
+    ro += dpp_f<kDppQuad2>(ro);
+    so += dpp_f<kDppQuad2>(so);
+    ro += dpp_f<kDppRor4>(ro);
+    so += dpp_f<kDppRor4>(so);
+    ro += dpp_f<kDppRor8>(ro);
+    so += dpp_f<kDppRor8>(so);
+    if (lpr >= 32) {
+        ro = add_xor16(ro);
+        so = add_xor16(so);
+    }
+    if (lpr >= 64) {
+        ro = add_xor32(ro);
+        so = add_xor32(so);
+    }
+}
+
+// Writes silu(g)*u of the kGateFR rows of one sub-wave item.
+__device__ __forceinline__ void gateup_epilogue(const float *g, const float *u, int lane,
+                                                uint32_t lpr, uint32_t rpi, uint32_t sub,
+                                                uint32_t cl, uint32_t item, uint32_t nrows,
+                                                float *act_row) {
+    static_assert(kGateFR == 4, "reduce-scatter layout assumes four rows per sub-wave");
+    if (lpr >= 16) {
+        float gv, uv;
+        rs4_pairs(g, u, lane, lpr, gv, uv);
+        if (cl < 4) {
+            const uint32_t j = (item * kGateFR + rs4_index(cl)) * rpi + sub;
+            // activation (elementwise.metal:8-17)
+            if (j < nrows) act_row[j] = gv / (1.0f + expf(-gv)) * uv;
+        }
+    } else {
+#pragma unroll
+        for (int f = 0; f < kGateFR; f++) {
+            const float gv = subwave_sum(g[f], (int)lpr), uv = subwave_sum(u[f], (int)lpr);
+            const uint32_t j = (item * kGateFR + f) * rpi + sub;
+            if (j < nrows && cl == 0) act_row[j] = gv / (1.0f + expf(-gv)) * uv;
+        }
+    }
+}
 constexpr int kDownFR = 2;    // output rows per sub-wave in decode_down
 
 // ------------------------------------------------------------------ pre --
+// One wave per block: router rows (and the shared expert's scalar gate row).
 template <int BR, int TR>
 __device__ __forceinline__ void router_item(const DecodeKArgs &a, uint32_t wave_id, uint32_t sub,
                                             uint32_t cl, const float *xr, float xsum) {
@@ -189,32 +271,10 @@ __device__ __forceinline__ void router_item(const DecodeKArgs &a, uint32_t wave_
     if (ok && cl == 0) a.logits[e] = a.logit_bias ? v + a.logit_bias[e] : v;
 }
 
-template <int BS, int ST>
-__device__ __forceinline__ void shared_item(const DecodeKArgs &a, uint32_t wave_id, uint32_t sub,
-                                            uint32_t cl, const float *xr, float xsum) {
-    // shared expert gate/up + SwiGLU (encode_dense, execute.rs:258-264)
-    const uint32_t lpr = a.lpr_h, rpi = 64u / lpr;
-    uint64_t rows[kSharedFR];
-    bool ok[kSharedFR];
-#pragma unroll
-    for (int f = 0; f < kSharedFR; f++) {
-        rows[f] = ((uint64_t)wave_id * kSharedFR + f) * rpi + sub;
-        ok[f] = rows[f] < a.ffs;
-    }
-    float g[kSharedFR], u[kSharedFR];
-    lane_rows_dot<BS, ST, kSharedFR>(a.sg, rows, ok, cl, a.h / 32, xr, xsum, g);
-    lane_rows_dot<BS, ST, kSharedFR>(a.su, rows, ok, cl, a.h / 32, xr, xsum, u);
-#pragma unroll
-    for (int f = 0; f < kSharedFR; f++) {
-        const float gv = subwave_sum(g[f], (int)lpr), uv = subwave_sum(u[f], (int)lpr);
-        if (ok[f] && cl == 0) a.sh_act[rows[f]] = gv / (1.0f + expf(-gv)) * uv;
-    }
-}
-
 template <int ST>
-__global__ __launch_bounds__(256) void decode_pre_kernel(DecodeKArgs a) {
-    const int lane = threadIdx.x & 63;
-    uint32_t wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
+__global__ __launch_bounds__(64) void decode_pre_kernel(DecodeKArgs a) {
+    const int lane = threadIdx.x;
+    const uint32_t wave_id = blockIdx.x;
     const uint32_t lpr = a.lpr_h, sub = lane / lpr, cl = lane % lpr;
     float xr[32];
     const float xsum = load_x_chunk(a.x, a.norm_w, a.eps, a.h, cl, (int)lpr, xr);
@@ -234,18 +294,7 @@ __global__ __launch_bounds__(256) void decode_pre_kernel(DecodeKArgs a) {
         }
         return;
     }
-    wave_id -= a.n_router_waves;
-    if (!a.has_shared) return;
-    if (wave_id < a.n_shared_waves) {
-        switch (a.sg.bits) {
-        case 2: shared_item<2, ST>(a, wave_id, sub, cl, xr, xsum); break;
-        case 4: shared_item<4, ST>(a, wave_id, sub, cl, xr, xsum); break;
-        default: shared_item<8, ST>(a, wave_id, sub, cl, xr, xsum); break;
-        }
-        return;
-    }
-    wave_id -= a.n_shared_waves;
-    if (wave_id == 0) {
+    if (a.has_shared && wave_id == a.n_router_waves) {
         // shared-expert gate input [h] -> scalar (matmul(shared_gate [h,1]),
         // execute.rs:230; weight reshaped [h] -> [h,1], loader.rs:194)
         float v = 0.f;
@@ -256,29 +305,57 @@ __global__ __launch_bounds__(256) void decode_pre_kernel(DecodeKArgs a) {
 }
 
 // --------------------------------------------------------------- gate/up --
+template <int BS, int ST>
+__device__ __forceinline__ void shared_item(const DecodeKArgs &a, uint32_t item, uint32_t sub,
+                                            uint32_t cl, const float *xr, float xsum) {
+    // shared expert gate/up + SwiGLU (encode_dense, execute.rs:258-264)
+    const uint32_t lpr = a.lpr_h, rpi = 64u / lpr;
+    uint64_t rows[kGateFR];
+    bool ok[kGateFR];
+#pragma unroll
+    for (int f = 0; f < kGateFR; f++) {
+        rows[f] = ((uint64_t)item * kGateFR + f) * rpi + sub;
+        ok[f] = rows[f] < a.ffs;
+    }
+    float g[kGateFR], u[kGateFR];
+    lane_rows_dot<BS, ST, kGateFR>(a.sg, rows, ok, cl, a.h / 32, xr, xsum, g);
+    lane_rows_dot<BS, ST, kGateFR>(a.su, rows, ok, cl, a.h / 32, xr, xsum, u);
+    gateup_epilogue(g, u, (int)(sub * lpr + cl), lpr, rpi, sub, cl, item, a.ffs, a.sh_act);
+}
+
+// One wave per block.  Waves [0, K*items) route the token (exactly, from the
+// logits) and then compute kGateFR*rpi SwiGLU outputs of one selected expert;
+// the remaining waves compute the shared expert's and need no routing, so
+// their loads overlap the others' routing.
 template <int BITS, int ST>
-__global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeKArgs a) {
-    extern __shared__ float route_vals[];  // E floats + K ids + K weights
-    uint32_t *s_ids = reinterpret_cast<uint32_t *>(route_vals + a.E);
-    float *s_w = route_vals + a.E + a.k;
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+__global__ __launch_bounds__(64) void decode_gateup_kernel(DecodeKArgs a) {
+    extern __shared__ float route_vals[];  // E floats (routing with E > 1024 only)
+    __shared__ uint32_t s_ids[64];
+    __shared__ float s_w[64];
+    const int lane = threadIdx.x;
     const uint32_t lpr = a.lpr_h, rpi = 64u / lpr, sub = lane / lpr, cl = lane % lpr;
+    const uint32_t wave_id = blockIdx.x;
+    const uint32_t routed_waves = a.k * a.n_gate_waves_per_expert;
     float xr[32];
     const float xsum = load_x_chunk(a.x, a.norm_w, a.eps, a.h, cl, (int)lpr, xr);
-    if (wv == 0) {
-        // route (sampling.metal:1-36), exact, redundantly per block
-        route_one_wave(route_vals, a.logits, a.E, a.k, (int)a.normalize, s_ids, s_w, lane);
-        if (blockIdx.x == 0 && lane == 0) {
-            for (uint32_t k = 0; k < a.k; k++) {
-                a.ids[k] = s_ids[k];
-                a.weights[k] = s_w[k];
-            }
+    if (wave_id >= routed_waves) {
+        if (!a.has_shared) return;
+        const uint32_t item = wave_id - routed_waves;
+        switch (a.sg.bits) {
+        case 2: shared_item<2, ST>(a, item, sub, cl, xr, xsum); break;
+        case 4: shared_item<4, ST>(a, item, sub, cl, xr, xsum); break;
+        default: shared_item<8, ST>(a, item, sub, cl, xr, xsum); break;
         }
+        return;
     }
+    // route (sampling.metal:1-36), exact, redundantly per wave
+    route_one_wave(route_vals, a.logits, a.E, a.k, (int)a.normalize, s_ids, s_w, lane);
     __syncthreads();
-    const uint32_t wave_id = blockIdx.x * 4 + wv;
+    if (wave_id == 0 && lane < a.k) {
+        a.ids[lane] = s_ids[lane];
+        a.weights[lane] = s_w[lane];
+    }
     const uint32_t kk = wave_id / a.n_gate_waves_per_expert;
-    if (kk >= a.k) return;
     const uint32_t item = wave_id % a.n_gate_waves_per_expert;
     const uint32_t e = s_ids[kk];  // < E by construction of route
     uint64_t rows[kGateFR];
@@ -292,24 +369,20 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeKArgs a) {
     float g[kGateFR], u[kGateFR];
     lane_rows_dot<BITS, ST, kGateFR>(a.gate, rows, ok, cl, a.h / 32, xr, xsum, g);
     lane_rows_dot<BITS, ST, kGateFR>(a.up, rows, ok, cl, a.h / 32, xr, xsum, u);
-#pragma unroll
-    for (int f = 0; f < kGateFR; f++) {
-        const float gv = subwave_sum(g[f], (int)lpr), uv = subwave_sum(u[f], (int)lpr);
-        const uint32_t j = (item * kGateFR + f) * rpi + sub;
-        // activation (elementwise.metal:8-17)
-        if (ok[f] && cl == 0) a.act[(uint64_t)kk * a.ff + j] = gv / (1.0f + expf(-gv)) * uv;
-    }
+    gateup_epilogue(g, u, lane, lpr, rpi, sub, cl, item, a.ff, a.act + (uint64_t)kk * a.ff);
 }
 
 // ------------------------------------------------------------------ down --
-// Block = 4 waves over `rows_per_block` output rows; wave w takes experts
-// w, w+4, ... of the K routed experts plus the shared one (index K), and the
-// four waves' partial sums meet in LDS.
+// Block = nw waves over `rows_per_block` output rows; wave w takes experts
+// w, w+nw, ... of the K routed experts plus the shared one (index K); all of
+// a wave's loads are issued before its arithmetic, and the waves' partial
+// sums meet in LDS.
+constexpr int kDownMaxWaves = 16;
+constexpr int kDownMaxPerWave = 2;
+
 template <int BITS, int ST>
-__device__ __forceinline__ void down_expert(const DecodeKArgs &a, const WDesc &w, uint32_t e,
-                                            const float *act_row, uint32_t row0, uint32_t sub,
-                                            uint32_t cl, uint32_t rpi, float *part) {
-    float xr[32];
+__device__ __forceinline__ void load_act_chunk(const float *act_row, uint32_t cl, float *xr,
+                                               float &xsum) {
     const float4 *src = reinterpret_cast<const float4 *>(act_row + (uint64_t)cl * 32);
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -319,57 +392,85 @@ __device__ __forceinline__ void down_expert(const DecodeKArgs &a, const WDesc &w
         xr[4 * i + 2] = v.z;
         xr[4 * i + 3] = v.w;
     }
-    float xsum = 0.f;
+    xsum = 0.f;
 #pragma unroll
     for (int j = 0; j < 32; j++) xsum += xr[j];
-    uint64_t rows[kDownFR];
-    bool ok[kDownFR];
+}
+
+template <int BITS, int ST, int BS>
+__device__ __forceinline__ void down_wave(const DecodeKArgs &a, uint32_t wv, uint32_t nw,
+                                          uint32_t row0, uint32_t sub, uint32_t cl, uint32_t rpi,
+                                          float *acc_r, float *acc_s) {
+    const uint32_t n_exp = a.k + (a.has_shared ? 1u : 0u);
+    const uint32_t C = a.ff / 32;
 #pragma unroll
-    for (int f = 0; f < kDownFR; f++) {
-        const uint32_t r = row0 + f * rpi + sub;
-        ok[f] = r < a.h;
-        rows[f] = (uint64_t)e * a.h + r;
+    for (int q = 0; q < kDownMaxPerWave; q++) {
+        const uint32_t kk = wv + q * nw;
+        if (kk >= n_exp) break;
+        uint64_t rows[kDownFR];
+        bool ok[kDownFR];
+        float xr[32], xsum, part[kDownFR];
+        if (kk < a.k) {
+            const uint32_t e = a.ids[kk];
+#pragma unroll
+            for (int f = 0; f < kDownFR; f++) {
+                const uint32_t r = row0 + f * rpi + sub;
+                ok[f] = r < a.h;
+                rows[f] = (uint64_t)e * a.h + r;
+            }
+            load_act_chunk<BITS, ST>(a.act + (uint64_t)kk * a.ff, cl, xr, xsum);
+            lane_rows_dot<BITS, ST, kDownFR>(a.down, rows, ok, cl, C, xr, xsum, part);
+            const float wk = a.weights[kk];
+#pragma unroll
+            for (int f = 0; f < kDownFR; f++) acc_r[f] += part[f] * wk;
+        } else {
+#pragma unroll
+            for (int f = 0; f < kDownFR; f++) {
+                const uint32_t r = row0 + f * rpi + sub;
+                ok[f] = r < a.h;
+                rows[f] = r;
+            }
+            load_act_chunk<BITS, ST>(a.sh_act, cl, xr, xsum);
+            lane_rows_dot<BS, ST, kDownFR>(a.sd, rows, ok, cl, C, xr, xsum, part);
+#pragma unroll
+            for (int f = 0; f < kDownFR; f++) acc_s[f] += part[f];
+        }
     }
-    lane_rows_dot<BITS, ST, kDownFR>(w, rows, ok, cl, a.ff / 32, xr, xsum, part);
 }
 
 template <int BITS, int ST>
-__global__ __launch_bounds__(256) void decode_down_kernel(DecodeKArgs a) {
-    __shared__ float red_r[4][128];
-    __shared__ float red_s[4][128];
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+__global__ __launch_bounds__(64 * kDownMaxWaves) void decode_down_kernel(DecodeKArgs a) {
+    __shared__ float red_r[kDownMaxWaves][128];
+    __shared__ float red_s[kDownMaxWaves][128];
+    const int lane = threadIdx.x & 63;
+    const uint32_t wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const uint32_t lpr = a.lpr_f, rpi = 64u / lpr, sub = lane / lpr, cl = lane % lpr;
     const uint32_t rows_per_block = rpi * kDownFR;
     const uint32_t row0 = blockIdx.x * rows_per_block;
     float acc_r[kDownFR], acc_s[kDownFR];
 #pragma unroll
     for (int f = 0; f < kDownFR; f++) acc_r[f] = acc_s[f] = 0.f;
-    const uint32_t n_exp = a.k + (a.has_shared ? 1u : 0u);
-    for (uint32_t kk = wv; kk < n_exp; kk += 4) {
-        float part[kDownFR];
-        if (kk < a.k) {
-            const uint32_t e = a.ids[kk];
-            down_expert<BITS, ST>(a, a.down, e, a.act + (uint64_t)kk * a.ff, row0, sub, cl, rpi,
-                                  part);
-            const float wk = a.weights[kk];
-#pragma unroll
-            for (int f = 0; f < kDownFR; f++) acc_r[f] += part[f] * wk;
-        } else {
-            switch (a.sd.bits) {
-            case 2: down_expert<2, ST>(a, a.sd, 0, a.sh_act, row0, sub, cl, rpi, part); break;
-            case 4: down_expert<4, ST>(a, a.sd, 0, a.sh_act, row0, sub, cl, rpi, part); break;
-            default: down_expert<8, ST>(a, a.sd, 0, a.sh_act, row0, sub, cl, rpi, part); break;
-            }
-#pragma unroll
-            for (int f = 0; f < kDownFR; f++) acc_s[f] += part[f];
-        }
+    switch (a.has_shared ? a.sd.bits : BITS) {
+    case 2: down_wave<BITS, ST, 2>(a, wv, nw, row0, sub, cl, rpi, acc_r, acc_s); break;
+    case 4: down_wave<BITS, ST, 4>(a, wv, nw, row0, sub, cl, rpi, acc_r, acc_s); break;
+    default: down_wave<BITS, ST, 8>(a, wv, nw, row0, sub, cl, rpi, acc_r, acc_s); break;
     }
+    static_assert(kDownFR == 2, "reduce-scatter layout assumes two rows per sub-wave");
+    if (lpr >= 16) {
+        float r, sh;
+        rs2_pairs(acc_r, acc_s, lane, lpr, r, sh);
+        if (cl < 2) {
+            red_r[wv][cl * rpi + sub] = r;
+            red_s[wv][cl * rpi + sub] = sh;
+        }
+    } else {
 #pragma unroll
-    for (int f = 0; f < kDownFR; f++) {
-        const float r = subwave_sum(acc_r[f], (int)lpr), s = subwave_sum(acc_s[f], (int)lpr);
-        if (cl == 0) {
-            red_r[wv][f * rpi + sub] = r;
-            red_s[wv][f * rpi + sub] = s;
+        for (int f = 0; f < kDownFR; f++) {
+            const float r = subwave_sum(acc_r[f], (int)lpr), sh = subwave_sum(acc_s[f], (int)lpr);
+            if (cl == 0) {
+                red_r[wv][f * rpi + sub] = r;
+                red_s[wv][f * rpi + sub] = sh;
+            }
         }
     }
     __syncthreads();
@@ -379,11 +480,12 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeKArgs a) {
             // mix (elementwise.metal:47-57), then shared / (1+exp(-g)) and add
             // (gate_scalar + add, execute.rs:231-232), then the residual
             // (execute.rs:236)
-            float v = red_r[0][i] + red_r[1][i] + red_r[2][i] + red_r[3][i];
-            if (a.has_shared) {
-                const float sv = red_s[0][i] + red_s[1][i] + red_s[2][i] + red_s[3][i];
-                v = v + sv / (1.0f + expf(-a.sh_gate[0]));
+            float v = 0.f, sv = 0.f;
+            for (uint32_t w = 0; w < nw; w++) {
+                v += red_r[w][i];
+                sv += red_s[w][i];
             }
+            if (a.has_shared) v = v + sv / (1.0f + expf(-a.sh_gate[0]));
             if (a.resid) v = a.resid[row] + v;
             a.out[row] = v;
         }
@@ -406,6 +508,8 @@ bool decode_supported(const DecodeArgs &a) {
     if (!pow2_chunks(g.in) || !pow2_chunks(g.out)) return false;
     if (a.router.bits && a.router.type != st) return false;
     if (a.router.out > 4096 || a.k == 0 || a.k > 64 || a.k > a.router.out) return false;
+    // the down kernel covers at most kDownMaxWaves * kDownMaxPerWave experts
+    if (a.k + (a.has_shared ? 1u : 0u) > (uint32_t)(kDownMaxWaves * kDownMaxPerWave)) return false;
     if (a.has_shared) {
         if (a.sg.bits == 0 || a.su.bits != a.sg.bits || a.sd.bits != a.sg.bits) return false;
         if (a.sg.type != st || a.su.type != st || a.sd.type != st) return false;
@@ -423,24 +527,25 @@ bool decode_supported(const DecodeArgs &a) {
 
 template <int BITS, int ST>
 static hipError_t launch_decode_t(Prof *p, hipStream_t s, const DecodeKArgs &k) {
-    const uint32_t pre_waves = k.n_router_waves + (k.has_shared ? k.n_shared_waves + 1 : 0);
+    const uint32_t pre_waves = k.n_router_waves + (k.has_shared ? 1 : 0);
     prof_begin(p, s, "decode_pre");
-    hipLaunchKernelGGL((decode_pre_kernel<ST>), dim3((pre_waves + 3) / 4), dim3(256), 0, s, k);
+    hipLaunchKernelGGL((decode_pre_kernel<ST>), dim3(pre_waves), dim3(64), 0, s, k);
     hipError_t e = hipGetLastError();
     prof_end(p, s);
     if (e != hipSuccess) return e;
-    const uint32_t gate_waves = k.k * k.n_gate_waves_per_expert;
-    const size_t lds = (size_t)(k.E + 2 * k.k) * sizeof(float);
+    const uint32_t gate_waves = k.k * k.n_gate_waves_per_expert + (k.has_shared ? k.n_shared_waves : 0);
+    const size_t lds = k.E > 1024 ? (size_t)k.E * sizeof(float) : 0;
     prof_begin(p, s, "decode_gateup");
-    hipLaunchKernelGGL((decode_gateup_kernel<BITS, ST>), dim3((gate_waves + 3) / 4), dim3(256), lds,
-                       s, k);
+    hipLaunchKernelGGL((decode_gateup_kernel<BITS, ST>), dim3(gate_waves), dim3(64), lds, s, k);
     e = hipGetLastError();
     prof_end(p, s);
     if (e != hipSuccess) return e;
     const uint32_t rows_per_block = (64u / k.lpr_f) * kDownFR;
+    const uint32_t n_exp = k.k + (k.has_shared ? 1u : 0u);
+    const uint32_t nw = n_exp < (uint32_t)kDownMaxWaves ? n_exp : (uint32_t)kDownMaxWaves;
     prof_begin(p, s, "decode_down");
     hipLaunchKernelGGL((decode_down_kernel<BITS, ST>), dim3((k.h + rows_per_block - 1) / rows_per_block),
-                       dim3(256), 0, s, k);
+                       dim3(64 * nw), 0, s, k);
     e = hipGetLastError();
     prof_end(p, s);
     return e;
@@ -455,7 +560,7 @@ hipError_t launch_decode(Prof *p, hipStream_t s, const DecodeArgs &a) {
     k.lpr_h = k.h / 32; k.lpr_f = k.ff / 32;
     const uint32_t rpi_h = 64u / k.lpr_h;
     k.n_router_waves = (k.E + rpi_h - 1) / rpi_h;
-    k.n_shared_waves = (k.ffs + rpi_h * kSharedFR - 1) / (rpi_h * kSharedFR);
+    k.n_shared_waves = (k.ffs + rpi_h * kGateFR - 1) / (rpi_h * kGateFR);
     k.n_gate_waves_per_expert = (k.ff + rpi_h * kGateFR - 1) / (rpi_h * kGateFR);
     k.x = a.x; k.norm_w = a.norm_w; k.eps = a.eps; k.logit_bias = a.logit_bias; k.resid = a.resid;
     k.out = a.out; k.logits = a.logits; k.ids = a.ids; k.weights = a.weights; k.act = a.act;
