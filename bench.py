@@ -74,6 +74,68 @@ def upload_layer(gpu, tensors):
     return BlockWeights(w[0], w[1], w[2], w[3], K, True, sh, gpu.weight_tensor(sgate))
 
 
+# ---- config 4: Qwen3-30B-A3B-shaped prefill (bf16 MFMA grouped GEMM) ----
+P_T, P_H, P_E, P_K, P_FF = 4096, 2048, 128, 8, 768
+PREFILL_FLOPS = 2 * P_T * P_K * 3 * P_H * P_FF          # 309,237,645,312 expert FLOPs
+ROUTER_FLOPS = 2 * P_T * P_H * P_E
+MFMA_PEAK = 2.5e15
+
+
+def zipf_bias(tokens, experts, seed, s=1.1):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    rank = np.empty(experts, np.float64)
+    rank[rng.permutation(experts)] = np.arange(1, experts + 1)
+    return np.broadcast_to((-s * np.log(rank)).astype(np.float32), (tokens, experts)).copy()
+
+
+def bench_prefill(gpu, iters=10):
+    """Config 4: one MoE layer over 4096 tokens, Zipf(1.1)-skewed routing."""
+    s = 600 * 100
+    router = Tensor.affine([P_H, P_E], *synth.random_affine(s + 1, P_H * P_E, 4, 64, BF16), 4, 64,
+                           BF16)
+    ex = [Tensor.affine(d, *synth.random_affine(s + 2 + i, int(np.prod(d)), 4, 64, BF16), 4, 64,
+                        BF16)
+          for i, d in enumerate(([P_H, P_FF, P_E], [P_H, P_FF, P_E], [P_FF, P_H, P_E]))]
+    w = [gpu.weight_tensor(t) for t in [router, *ex]]
+    bw = BlockWeights(w[0], w[1], w[2], w[3], P_K, True)
+    x = gpu.upload(synth.normal(6060, P_T * P_H))
+    out = gpu.zeros(P_T * P_H)
+    ws = gpu.zeros(bw.workspace_elems(P_T))
+    bias = gpu.upload(zipf_bias(P_T, P_E, 4))
+    ids = gpu.zeros(P_T * P_K)
+    for _ in range(2):
+        with gpu.batch() as b:
+            b.moe_block(bw, x, out, P_T, ws, logit_bias=bias, ids_out=ids)
+    gpu.profile_reset()
+    gpu.profile(True)
+    with gpu.batch() as b:
+        b.moe_block(bw, x, out, P_T, ws, logit_bias=bias, ids_out=ids)
+    prof = gpu.profile_read()
+    gpu.profile(False)
+    with gpu.batch() as b:
+        for _ in range(iters):
+            b.moe_block(bw, x, out, P_T, ws, logit_bias=bias, ids_out=ids)
+    t = b.seconds / iters
+    counts = np.bincount(gpu.read_u32(ids), minlength=P_E)
+    k_us = {k: round(v[1] / v[0] * 1e6, 2) for k, v in prof.items()}
+    expert_s = sum(v[1] / v[0] for k, v in prof.items() if k in ("mfma_gateup", "mfma_down"))
+    for buf in (x, out, ws, bias, ids):
+        gpu.release(buf)
+    return {
+        "workload": "config4: Qwen3-30B-A3B MoE layer prefill, 4096 tokens (h2048 E128 top8 "
+                    "ff768, 4-bit g64 bf16, Zipf(1.1) router skew), path bf16 MFMA",
+        "tokens_per_s": round(P_T / t, 1),
+        "ms_per_layer": round(t * 1e3, 4),
+        "expert_flops": PREFILL_FLOPS,
+        "achieved_TFLOPs": round(PREFILL_FLOPS / t / 1e12, 2),
+        "mfma_frac": round(PREFILL_FLOPS / t / MFMA_PEAK, 4),
+        "expert_kernels_TFLOPs": round(PREFILL_FLOPS / expert_s / 1e12, 2) if expert_s else None,
+        "expert_kernels_mfma_frac": round(PREFILL_FLOPS / expert_s / MFMA_PEAK, 4) if expert_s else None,
+        "segment_max": int(counts.max()), "segment_min": int(counts.min()),
+        "kernels_us": k_us,
+    }
+
+
 def cpu_baseline(tensors, budget_s):
     """The C oracle (single thread) on the same layer, bounded sample."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -102,6 +164,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=640)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -206,6 +269,11 @@ def main():
         "roofline": roof,
         "cpu_baseline": None,
     }
+    if not args.no_prefill:
+        log("[bench] config-4 prefill (bf16 MFMA)")
+        result["prefill"] = bench_prefill(gpu)
+        log(f"[bench] prefill: {result['prefill']['ms_per_layer']} ms/layer, "
+            f"{result['prefill']['achieved_TFLOPs']} TFLOP/s")
     if not args.no_cpu:
         log("[bench] timing the CPU oracle")
         result["cpu_baseline"] = cpu_baseline(host0, args.cpu_seconds)

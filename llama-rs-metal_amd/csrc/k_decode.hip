@@ -332,6 +332,7 @@ __global__ __launch_bounds__(64) void decode_gateup_kernel(DecodeKArgs a) {
     extern __shared__ float route_vals[];  // E floats (routing with E > 1024 only)
     __shared__ uint32_t s_ids[64];
     __shared__ float s_w[64];
+    __shared__ RouteLds route_lds;
     const int lane = threadIdx.x;
     const uint32_t lpr = a.lpr_h, rpi = 64u / lpr, sub = lane / lpr, cl = lane % lpr;
     const uint32_t wave_id = blockIdx.x;
@@ -349,7 +350,7 @@ __global__ __launch_bounds__(64) void decode_gateup_kernel(DecodeKArgs a) {
         return;
     }
     // route (sampling.metal:1-36), exact, redundantly per wave
-    route_one_wave(route_vals, a.logits, a.E, a.k, (int)a.normalize, s_ids, s_w, lane);
+    route_one_wave(&route_lds, route_vals, a.logits, a.E, a.k, (int)a.normalize, s_ids, s_w, lane);
     __syncthreads();
     if (wave_id == 0 && lane < a.k) {
         a.ids[lane] = s_ids[lane];
@@ -447,6 +448,8 @@ __global__ __launch_bounds__(64 * kDownMaxWaves) void decode_down_kernel(DecodeK
     const uint32_t lpr = a.lpr_f, rpi = 64u / lpr, sub = lane / lpr, cl = lane % lpr;
     const uint32_t rows_per_block = rpi * kDownFR;
     const uint32_t row0 = blockIdx.x * rows_per_block;
+    // issued first: needed only after the LDS combine
+    const float shared_gate = a.has_shared ? a.sh_gate[0] : 0.f;
     float acc_r[kDownFR], acc_s[kDownFR];
 #pragma unroll
     for (int f = 0; f < kDownFR; f++) acc_r[f] = acc_s[f] = 0.f;
@@ -485,7 +488,7 @@ __global__ __launch_bounds__(64 * kDownMaxWaves) void decode_down_kernel(DecodeK
                 v += red_r[w][i];
                 sv += red_s[w][i];
             }
-            if (a.has_shared) v = v + sv / (1.0f + expf(-a.sh_gate[0]));
+            if (a.has_shared) v = v + sv / (1.0f + expf(-shared_gate));
             if (a.resid) v = a.resid[row] + v;
             a.out[row] = v;
         }

@@ -10,8 +10,9 @@ __global__ __launch_bounds__(64) void route_kernel(const float *__restrict__ log
                                                    uint32_t *__restrict__ ids,
                                                    float *__restrict__ weights) {
     extern __shared__ float vals[];
+    __shared__ RouteLds L;
     const uint32_t t = blockIdx.x;
-    route_one_wave(vals, logits + (uint64_t)t * E, E, K, normalize, ids + (uint64_t)t * K,
+    route_one_wave(&L, vals, logits + (uint64_t)t * E, E, K, normalize, ids + (uint64_t)t * K,
                    weights + (uint64_t)t * K, threadIdx.x);
 }
 

@@ -12,7 +12,7 @@ namespace {
 
 struct WsLayout {
     uint64_t logits, ids, weights, counts, offsets, perm, pos, act, yexp, sh_act, sh_up, sh_gate,
-        sh_out, xnorm, gates, ups, eo, proj, sgv, total;
+        sh_out, xnorm, gates, ups, eo, proj, sgv, xb16, act16, y16, tiles, ntiles, total;
 };
 
 inline uint64_t al64(uint64_t n) { return (n + 63) & ~63ull; }
@@ -43,6 +43,12 @@ WsLayout ws_layout(uint64_t T, uint64_t E, uint64_t K, uint64_t h, uint64_t ff, 
     take(L.eo, K * h);
     take(L.proj, h);
     take(L.sgv, 1);
+    // bf16 MFMA path (two bf16 per 4-byte element)
+    take(L.xb16, (T * h + 1) / 2);
+    take(L.act16, (T * K * ff + 1) / 2);
+    take(L.y16, (T * K * h + 1) / 2);
+    take(L.tiles, 2 * ((T * K + 127) / 128 + E + 1));
+    take(L.ntiles, 1);
     L.total = o;
     return L;
 }
@@ -182,6 +188,59 @@ moe_status run_grouped(moe_gpu *g, const moe_block_weights *w, const Dims &d, co
     return MOE_OK;
 }
 
+bool mfma_path_ok(const moe_block_weights *w, const Dims &d) {
+    const WDesc G = wdesc(w->gate), U = wdesc(w->up), D = wdesc(w->down);
+    return mfma_supported(G) && mfma_supported(U) && mfma_supported(D) && G.bits == U.bits &&
+           G.type == U.type && d.h % 128 == 0 && d.ff % 128 == 0;
+}
+
+// bf16 MFMA grouped path (prefill-sized expert segments).
+moe_status run_mfma(moe_gpu *g, const moe_block_weights *w, const Dims &d, const float *xraw,
+                    const float *nw, float eps, float *out, uint64_t T, const moe_block_io *io,
+                    const WsLayout &L, float *ws, float *logits, uint32_t *ids, float *wts) {
+    Prof *p = &g->prof;
+    hipStream_t s = g->stream;
+    const uint32_t K = (uint32_t)d.K, E = (uint32_t)d.E;
+    uint16_t *xb16 = reinterpret_cast<uint16_t *>(ws + L.xb16);
+    uint16_t *act16 = reinterpret_cast<uint16_t *>(ws + L.act16);
+    uint16_t *y16 = reinterpret_cast<uint16_t *>(ws + L.y16);
+    uint32_t *counts = reinterpret_cast<uint32_t *>(ws + L.counts);
+    uint32_t *offsets = reinterpret_cast<uint32_t *>(ws + L.offsets);
+    uint32_t *perm = reinterpret_cast<uint32_t *>(ws + L.perm);
+    uint32_t *pos = reinterpret_cast<uint32_t *>(ws + L.pos);
+    uint32_t *tiles = reinterpret_cast<uint32_t *>(ws + L.tiles);
+    uint32_t *ntiles = reinterpret_cast<uint32_t *>(ws + L.ntiles);
+    float *xn = nw ? ws + L.xnorm : nullptr;
+    TRY(launch_to_bf16(p, s, xraw, nw, eps, (uint32_t)T, (uint32_t)d.h, xb16, xn));
+    const float *xin = nw ? xn : xraw;  // F32 input of the VALU products
+    const WDesc R = wdesc(w->router);
+    const float *bias = has(io->logit_bias) ? fp(io->logit_bias) : nullptr;
+    if (mfma_supported(R)) {
+        TRY(launch_mfma_router(p, s, R, xb16, (uint32_t)T, bias, logits));
+    } else {
+        TRY(launch_gemv(p, s, R, xin, 0, nullptr, 1, logits, (uint32_t)T));
+        if (bias) TRY(launch_add(p, s, logits, bias, logits, T * d.E));
+    }
+    TRY(launch_route(p, s, logits, E, K, w->normalize ? 1 : 0, (uint32_t)T, ids, wts));
+    TRY(launch_dispatch(p, s, ids, (uint32_t)(T * K), E, counts, offsets, perm, pos));
+    TRY(launch_mfma_experts(p, s, wdesc(w->gate), wdesc(w->up), wdesc(w->down), xb16, offsets, perm,
+                            wts, K, (uint32_t)(T * K), tiles, ntiles, act16, y16));
+    const float *so = nullptr, *sgv = nullptr;
+    if (w->has_shared) {
+        float *sg = ws + L.sh_act, *su = ws + L.sh_up, *sout = ws + L.sh_out, *sgt = ws + L.sh_gate;
+        TRY(launch_gemv(p, s, wdesc(w->shared_gate), xin, 0, nullptr, 1, sg, (uint32_t)T));
+        TRY(launch_gemv(p, s, wdesc(w->shared_up), xin, 0, nullptr, 1, su, (uint32_t)T));
+        TRY(launch_swiglu(p, s, sg, su, sg, T * d.ffs));
+        TRY(launch_gemv(p, s, wdesc(w->shared_down), sg, 0, nullptr, 1, sout, (uint32_t)T));
+        TRY(launch_gemv(p, s, gate_inp_desc(w->shared_gate_inp), xin, 0, nullptr, 1, sgt, (uint32_t)T));
+        so = sout;
+        sgv = sgt;
+    }
+    TRY(launch_combine16(p, s, y16, pos, K, so, sgv, io->residual ? xraw : nullptr, out, (uint32_t)T,
+                         (uint32_t)d.h));
+    return MOE_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -213,7 +272,9 @@ moe_status moe_block(moe_gpu *g, const moe_block_weights *w, moe_buffer x, moe_b
     if (has(io->norm_weight) &&
         (io->norm_weight.len != d.h || !std::isfinite(io->norm_eps) || io->norm_eps <= 0.f))
         return shape(g, "norm");
-    if (io->path > MOE_PATH_GROUPED) return shape(g, "unknown path");
+    if (io->path > MOE_PATH_MFMA) return shape(g, "unknown path");
+    if (io->path == MOE_PATH_MFMA && !mfma_path_ok(w, d))
+        return shape(g, "MFMA path needs hidden and ff multiples of 128 and supported weight kinds");
     // ownership
     std::vector<Range> reads{rng(x)};
     std::vector<Range> writes{rng(out), rng(io->workspace)};
@@ -281,6 +342,10 @@ moe_status moe_block(moe_gpu *g, const moe_block_weights *w, moe_buffer x, moe_b
         a.sh_gate = ws + L.sh_gate;
         if (decode_supported(a)) return launched(g, launch_decode(&g->prof, g->stream, a), "decode");
     }
+
+    const bool mean_seg_16 = T * d.K >= 16 * d.E;  // mean expert segment >= 16 pairs
+    if (io->path == MOE_PATH_MFMA || (io->path == MOE_PATH_AUTO && mean_seg_16 && mfma_path_ok(w, d)))
+        return run_mfma(g, w, d, xraw, nw, io->norm_eps, o, T, io, L, ws, logits, ids, wts);
 
     const float *xin = xraw;
     if (nw) {

@@ -90,6 +90,21 @@ hipError_t launch_grouped_down(Prof *p, hipStream_t s, const WDesc &down, const 
                                const uint32_t *offsets, uint32_t experts, uint32_t pairs,
                                float *yexp);
 
+// ---- bf16 MFMA grouped products (k_mfma.hip) ----
+bool mfma_supported(const WDesc &w);
+hipError_t launch_to_bf16(Prof *p, hipStream_t s, const float *x, const float *norm_w, float eps,
+                          uint32_t tokens, uint32_t h, uint16_t *y, float *xn);
+hipError_t launch_mfma_router(Prof *p, hipStream_t s, const WDesc &r, const uint16_t *xb16,
+                              uint32_t tokens, const float *bias, float *logits);
+hipError_t launch_mfma_experts(Prof *p, hipStream_t s, const WDesc &gate, const WDesc &up,
+                               const WDesc &down, const uint16_t *xb16, const uint32_t *offsets,
+                               const uint32_t *perm, const float *route_w, uint32_t k,
+                               uint32_t pairs, uint32_t *tiles, uint32_t *ntiles,
+                               uint16_t *act16, uint16_t *y16);
+hipError_t launch_combine16(Prof *p, hipStream_t s, const uint16_t *y16, const uint32_t *pos,
+                            uint32_t k, const float *sh_out, const float *sh_gate,
+                            const float *resid, float *out, uint32_t tokens, uint32_t h);
+
 // ---- fused single-token decode (k_decode.hip) ----
 struct DecodeArgs {
     WDesc router, gate, up, down, sg, su, sd, sgi;

@@ -83,6 +83,113 @@ __device__ __forceinline__ void route_wave_regs(const float *__restrict__ logits
     }
 }
 
+// LDS scratch of one routing wave.
+struct RouteLds {
+    uint64_t mk[64];  // composite keys of the 64 lanes' local bests
+    uint64_t ck[64];  // composite keys of the surviving candidates
+    uint32_t sj[64];  // selected ids by rank
+    float sv[64];     // selected logits by rank
+};
+
+// Composite selection key: larger = earlier in the reference's scan order
+// (logit descending, index ascending); E < 65536.
+__device__ __forceinline__ uint64_t ckey(float v, uint32_t j) {
+    return ((uint64_t)fkey(v) << 16) | (uint64_t)(0xffffu - j);
+}
+__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+// LDS writes of this wave are complete and visible to its other lanes.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+}
+
+// Same selection as route_wave_regs without K serial passes (K <= 64):
+//  1. every lane finds its local best (strict `>` over ascending j);
+//  2. t = the K-th best of the 64 lane bests under the composite order: at
+//     least K elements are >= t, so every top-K element has logit >= t;
+//  3. the elements with logit >= t (NaN and -inf excluded) are compacted,
+//     and each is ranked against the others under the composite order.
+// Returns false (nothing written) when more than 64 candidates survive; the
+// caller then runs route_wave_regs.
+template <int R>
+__device__ __forceinline__ bool route_wave_rank(RouteLds *L, const float *__restrict__ logits,
+                                                uint32_t E, uint32_t K, int normalize,
+                                                uint32_t *ids, float *weights, int lane) {
+    float v[R];
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        const uint32_t j = lane + kWave * i;
+        v[i] = j < E ? logits[j] : -INFINITY;
+    }
+    float lm = -INFINITY, m = -INFINITY;
+    int li = R;
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        if (v[i] > lm) {
+            lm = v[i];
+            li = i;
+        }
+        m = fmaxf(m, v[i]);
+    }
+    const uint64_t my = li < R ? ckey(lm, lane + kWave * li) : 0ull;
+    L->mk[lane] = my;
+    const float mx = wave_max(m);
+    float den = 0.f;
+#pragma unroll
+    for (int i = 0; i < R; i++)
+        if (lane + kWave * i < E) den += expf(v[i] - mx);
+    wave_lds_sync();
+    uint32_t rank = 0;
+#pragma unroll
+    for (int c = 0; c < kWave; c++) rank += L->mk[c] > my ? 1u : 0u;
+    den = wave_sum(den);
+    const uint64_t tm = __ballot(rank == K - 1);
+    uint32_t tval = 0;  // no lane at rank K-1: fewer than K lane bests -> keep all
+    if (tm) tval = (uint32_t)(readlane_u((uint32_t)(my >> 32), __ffsll((unsigned long long)tm) - 1) << 16 |
+                              readlane_u((uint32_t)my, __ffsll((unsigned long long)tm) - 1) >> 16);
+    uint32_t total = 0, pos[R];
+    bool q[R];
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        q[i] = v[i] > -INFINITY && fkey(v[i]) >= tval;
+        const uint64_t bm = __ballot(q[i]);
+        pos[i] = total + lanes_below(bm);
+        total += (uint32_t)__popcll(bm);
+    }
+    if (total > (uint32_t)kWave) return false;
+#pragma unroll
+    for (int i = 0; i < R; i++)
+        if (q[i]) L->ck[pos[i]] = ckey(v[i], lane + kWave * i);
+    wave_lds_sync();
+    const uint64_t mine = (uint32_t)lane < total ? L->ck[lane] : 0ull;
+    uint32_t r = 0;
+    for (uint32_t c = 0; c < total; c += 2) {
+        const uint64_t c0 = L->ck[c], c1 = c + 1 < total ? L->ck[c + 1] : 0ull;
+        r += (c0 > mine ? 1u : 0u) + (c1 > mine ? 1u : 0u);
+    }
+    if ((uint32_t)lane < total && r < K) {
+        L->sj[r] = 0xffffu - (uint32_t)(mine & 0xffffu);
+        L->sv[r] = funkey((uint32_t)(mine >> 16));
+    }
+    wave_lds_sync();
+    float score = -INFINITY;  // ranks beyond the candidates: id 0, score -inf
+    uint32_t id = 0;
+    if ((uint32_t)lane < K && (uint32_t)lane < total) {
+        score = L->sv[lane];
+        id = L->sj[lane];
+    }
+    float wk = (uint32_t)lane < K ? expf(score - mx) / den : 0.f;
+    if (normalize) wk = wk / wave_sum(wk);
+    if ((uint32_t)lane < K) {
+        ids[lane] = id;
+        weights[lane] = wk;
+    }
+    return true;
+}
+
 // Same selection for E > 1024 with the logits in this wave's LDS slice
 // `vals` (E floats); a selected entry is overwritten with -inf, which removes
 // it exactly as the reference's `used` test does (an entry equal to -inf can
@@ -129,23 +236,31 @@ __device__ __forceinline__ void route_wave_lds(float *vals, const float *__restr
         for (uint32_t k = 0; k < K; k++) weights[k] /= selected;
 }
 
-// Routing of one token by one wave; `vals` (E floats of LDS) is only used
-// when E > 1024 or K > 64.
-__device__ __forceinline__ void route_one_wave(float *vals, const float *__restrict__ logits,
-                                               uint32_t E, uint32_t K, int normalize,
-                                               uint32_t *ids, float *weights, int lane) {
+// Routing of one token by one wave (LDS scratch `L`); `vals` (E floats of
+// LDS) is only used when E > 1024 or K > 64.
+template <int R>
+__device__ __forceinline__ void route_regs(RouteLds *L, const float *__restrict__ logits,
+                                           uint32_t E, uint32_t K, int normalize, uint32_t *ids,
+                                           float *weights, int lane) {
+    if (!route_wave_rank<R>(L, logits, E, K, normalize, ids, weights, lane))
+        route_wave_regs<R>(logits, E, K, normalize, ids, weights, lane);
+}
+__device__ __forceinline__ void route_one_wave(RouteLds *L, float *vals,
+                                               const float *__restrict__ logits, uint32_t E,
+                                               uint32_t K, int normalize, uint32_t *ids,
+                                               float *weights, int lane) {
     if (K > (uint32_t)kWave || E > 1024)
         route_wave_lds(vals, logits, E, K, normalize, ids, weights, lane);
     else if (E <= 64)
-        route_wave_regs<1>(logits, E, K, normalize, ids, weights, lane);
+        route_regs<1>(L, logits, E, K, normalize, ids, weights, lane);
     else if (E <= 128)
-        route_wave_regs<2>(logits, E, K, normalize, ids, weights, lane);
+        route_regs<2>(L, logits, E, K, normalize, ids, weights, lane);
     else if (E <= 256)
-        route_wave_regs<4>(logits, E, K, normalize, ids, weights, lane);
+        route_regs<4>(L, logits, E, K, normalize, ids, weights, lane);
     else if (E <= 512)
-        route_wave_regs<8>(logits, E, K, normalize, ids, weights, lane);
+        route_regs<8>(L, logits, E, K, normalize, ids, weights, lane);
     else
-        route_wave_regs<16>(logits, E, K, normalize, ids, weights, lane);
+        route_regs<16>(L, logits, E, K, normalize, ids, weights, lane);
 }
 
 }  // namespace moehip

@@ -3,12 +3,12 @@
 `api` mirrors metal_backend's Gpu / Batch op surface over libmoe_hip.so;
 `synth` builds the seeded synthetic inputs of the benchmark configurations.
 """
-from .api import (BF16, F16, F32, PATH_AUTO, PATH_GROUPED, PATH_OPS, SIGNATURES, AllocationError,
+from .api import (BF16, F16, F32, PATH_AUTO, PATH_GROUPED, PATH_MFMA, PATH_OPS, SIGNATURES, AllocationError,
                   Batch, BlockWeights, Buffer, Gpu, GpuError, MoeError, ShapeError, Tensor,
                   UnavailableError, Weight, load_library, LIB_PATH)
 
 __all__ = [
-    "BF16", "F16", "F32", "PATH_AUTO", "PATH_GROUPED", "PATH_OPS", "SIGNATURES",
+    "BF16", "F16", "F32", "PATH_AUTO", "PATH_GROUPED", "PATH_MFMA", "PATH_OPS", "SIGNATURES",
     "AllocationError", "Batch", "BlockWeights", "Buffer", "Gpu", "GpuError", "MoeError",
     "ShapeError", "Tensor", "UnavailableError", "Weight", "load_library", "LIB_PATH",
 ]

@@ -23,7 +23,7 @@ PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(PKG_DIR, "libmoe_hip.so")
 
 F32, F16, BF16 = 0, 1, 30  # crates/model-format/src/dtype.rs:5-15
-PATH_AUTO, PATH_OPS, PATH_GROUPED = 0, 1, 2
+PATH_AUTO, PATH_OPS, PATH_GROUPED, PATH_MFMA = 0, 1, 2, 3
 
 
 # --------------------------------------------------------------- errors --

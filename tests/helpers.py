@@ -96,6 +96,12 @@ def config3(seed=45):
     return HostBlock(2048, 512, 10, 512, 512, kinds, seed=seed, random_experts=True)
 
 
+def config4(seed=46):
+    """Config 4: Qwen3-30B-A3B-shaped prefill layer, 4-bit g64 everywhere, no shared expert."""
+    kinds = {"router": (4, 64, BF16), "experts": (4, 64, BF16)}
+    return HostBlock(2048, 128, 8, 768, 0, kinds, seed=seed, random_experts=True)
+
+
 def config5(variant, seed=47):
     """Config 5 layer: config-2 shapes with 2-bit g32 or 8-bit g128 experts."""
     q = (2, 32, BF16) if variant == "2bit" else (8, 128, BF16)

@@ -10,12 +10,14 @@ import numpy as np
 import pytest
 
 import oracle
-from helpers import close, config1, config2, config3, config5, hot_bias, rel_max_err
-from hip_backend import PATH_AUTO, PATH_GROUPED, PATH_OPS, synth
+from helpers import (close, config1, config2, config3, config4, config5, hot_bias, rel_max_err,
+                     zipf_bias)
+from hip_backend import PATH_AUTO, PATH_GROUPED, PATH_MFMA, PATH_OPS, synth
 
 pytestmark = pytest.mark.gpu
 
 F32_TOL = 1e-4
+BF16_TOL = 2e-2  # bf16-MFMA prefill path
 
 
 def run_block(gpu, bw, x, T, path=PATH_AUTO, bias=None, norm_w=None, residual=False):
@@ -38,7 +40,7 @@ def run_block(gpu, bw, x, T, path=PATH_AUTO, bias=None, norm_w=None, residual=Fa
 
 
 def check_against_oracle(blk, x, got, tokens=None, bias=None, tol=F32_TOL, norm_w=None,
-                         residual=False):
+                         residual=False, logit_tol=1e-5):
     out, logits, ids, wts = got
     T = x.shape[0]
     rows = range(T) if tokens is None else tokens
@@ -50,7 +52,7 @@ def check_against_oracle(blk, x, got, tokens=None, bias=None, tol=F32_TOL, norm_
     ref_logits = np.stack([oracle.matmul(blk.router, xin[t], 1) for t in sel])
     if bias is not None:
         ref_logits = ref_logits + bias[sel]
-    assert rel_max_err(logits[sel], ref_logits) < 1e-5
+    assert rel_max_err(logits[sel], ref_logits) < logit_tol
     # routing + experts on the GPU's logits
     ref_out, _, ref_ids, ref_w = oracle.moe_block(blk.spec(), xin[sel], len(sel),
                                                   logits_in=logits[sel])
@@ -186,3 +188,45 @@ def test_in_place_residual_stream(gpu, c2):
         b.moe_block(bw, hb, hb, 1, ws, residual=True)
     ref = run_block(gpu, bw, x.reshape(1, -1), 1, PATH_AUTO)[0].ravel()
     close(gpu.read(hb), x + ref, 1e-6)
+
+
+# ------------------------------------------------------- config 4 (MFMA) --
+@pytest.fixture(scope="module")
+def c4(gpu):
+    blk = config4()
+    return blk, blk.upload(gpu)
+
+
+def test_config4_prefill_mfma_zipf(gpu, c4):
+    blk, bw = c4
+    T = 4096
+    print("[case] config4 prefill T=4096 (auto -> bf16 MFMA)", flush=True)
+    x = synth.normal(4000, T * 2048).reshape(T, 2048)
+    bias = zipf_bias(T, 128, seed=4)
+    got = run_block(gpu, bw, x, T, PATH_AUTO, bias=bias)
+    sample = list(range(0, T, 256)) + [T - 1]
+    err = check_against_oracle(blk, x, got, tokens=sample, bias=bias, tol=BF16_TOL,
+                               logit_tol=BF16_TOL)
+    print(f"[case] config4 rel err {err:.3e}", flush=True)
+    counts = np.bincount(got[2].ravel(), minlength=128)
+    assert counts.max() > 8 * counts.mean()  # the Zipf skew is realised
+
+
+def test_mfma_path_with_shared_expert(gpu, c2):
+    blk, bw = c2
+    T = 256
+    print("[case] config2 shapes T=256 forced MFMA", flush=True)
+    x = synth.normal(4100, T * 2048).reshape(T, 2048)
+    got = run_block(gpu, bw, x, T, PATH_MFMA)
+    check_against_oracle(blk, x, got, tokens=range(0, T, 37), tol=BF16_TOL, logit_tol=BF16_TOL)
+
+
+def test_mfma_path_8bit_router_norm_residual(gpu, c3):
+    blk, bw = c3
+    T = 64
+    x = synth.normal(4200, T * 2048).reshape(T, 2048)
+    nw = (1.0 + 0.1 * synth.normal(4201, 2048)).astype(np.float32)
+    bias = hot_bias(T, 512, seed=7)
+    got = run_block(gpu, bw, x, T, PATH_MFMA, bias=bias, norm_w=nw, residual=True)
+    check_against_oracle(blk, x, got, tokens=range(0, T, 9), bias=bias, tol=BF16_TOL,
+                         norm_w=nw, residual=True, logit_tol=BF16_TOL)
