@@ -157,6 +157,48 @@ def cpu_baseline(tensors, budget_s):
                       f"oracle/moe_oracle.c orc_moe_block, single thread, {el:.1f} s"}
 
 
+COPY_BYTES = 256 << 20  # calibration copy: reads and writes 256 MiB
+
+
+def traffic_probe(gpu, which):
+    """Eager workload for HBM-traffic counters (rocprofv3 --pmc FETCH_SIZE /
+    WRITE_SIZE): a few launches of the named path, then a plain copy kernel of
+    COPY_BYTES (reads COPY_BYTES, writes COPY_BYTES) whose counter readings
+    calibrate the scale of the counters."""
+    src = gpu.zeros(COPY_BYTES // 4)
+    dst = gpu.zeros(COPY_BYTES // 4)
+    if which == "decode":
+        layers = [upload_layer(gpu, make_layer_tensors(500 + l)) for l in range(LAYERS)]
+        xs = gpu.upload(synth.normal(4242, CHUNK * H))
+        outs = gpu.zeros(CHUNK * H)
+        ws = gpu.zeros(layers[0].workspace_elems(1))
+        with gpu.batch() as b:
+            for j in range(CHUNK):
+                b.moe_block(layers[j % LAYERS], xs.view(j * H, H), outs.view(j * H, H), 1, ws)
+        log(f"[probe] {CHUNK} eager config-2 decode steps done")
+    else:
+        bench_prefill(gpu, iters=1)
+        log("[probe] config-4 prefill done")
+    with gpu.batch() as b:
+        for _ in range(4):
+            b.copy(src, dst)
+    log(f"[probe] 4 copies of {COPY_BYTES} bytes done")
+
+
+def committed_traffic(kernel_prefix):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 --pmc
+    summary (profiles/traffic.json), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        kernels = json.load(f).get("kernels", {})
+    for name, v in kernels.items():
+        if name.startswith(kernel_prefix):
+            return v.get("bytes_per_launch")
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -165,6 +207,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--traffic-probe", choices=["decode", "prefill"], default=None,
+                    help="short eager workload for rocprofv3 --pmc runs (no timing output)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -174,6 +218,10 @@ def main():
     warm = max(CHUNK, (args.warmup + CHUNK - 1) // CHUNK * CHUNK)
 
     gpu = Gpu(0)
+    if args.traffic_probe:
+        traffic_probe(gpu, args.traffic_probe)
+        gpu.close()
+        return
     log(f"[bench] device {gpu.name}; building {LAYERS} config-2 layers")
     layers, host0 = [], None
     for l in range(LAYERS):
@@ -236,12 +284,10 @@ def main():
                 "unit": "GB/s", "frac": round(achieved * 1e9 / HBM_PEAK, 4), "traffic": None,
                 "kernel": dom, "algorithmic_bytes_per_launch": GATEUP_BYTES,
                 "avg_launch_us": round(dom_s * 1e6, 3)}
-        tpath = os.path.join(ROOT, "profiles", "traffic_decode_gateup.json")
-        if os.path.exists(tpath):
-            with open(tpath) as f:
-                tr = json.load(f)
-            roof["traffic"] = tr.get("bytes_per_launch")
-            roof["traffic_source"] = "profiles/traffic_decode_gateup.json"
+        traffic = committed_traffic("decode_gateup_kernel")
+        if traffic:
+            roof["traffic"] = traffic
+            roof["traffic_source"] = "profiles/traffic.json (rocprofv3 --pmc, calibrated)"
 
     layer_gbps = EXPERT_BYTES_PER_TOKEN / per_step / 1e9
     result = {
