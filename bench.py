@@ -37,7 +37,7 @@ H, E, K, FF, FFS, BITS, GROUP = 2048, 512, 10, 512, 512, 4, 64
 MAT_BYTES = FF * H * BITS // 8 + 2 * (FF * H // GROUP) * 2          # 589,824
 EXPERT_BYTES_PER_TOKEN = K * 3 * MAT_BYTES + 3 * MAT_BYTES          # 19,464,192
 ROUTER_BYTES = H * E * 4 + H * 4                                    # F32 router + gate row
-GATEUP_BYTES = K * 2 * MAT_BYTES                                    # decode_gateup per launch
+GATEUP_BYTES = K * 2 * MAT_BYTES + 2 * MAT_BYTES                    # decode_gateup per launch (routed + shared gate/up)
 HBM_PEAK = 8.0e12
 CHUNK = 64       # steps per captured graph
 LAYERS = 8       # distinct weight sets rotated

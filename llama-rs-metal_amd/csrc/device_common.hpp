@@ -189,6 +189,21 @@ __device__ __forceinline__ float word_dot(uint32_t w, const float *x) {
     return d;
 }
 
+// e^x from the hardware base-2 exponential (v_exp_f32, 1 ulp): x*log2(e) is
+// split into its rounded product t and that product's rounding error (an
+// FMA recovers it, plus the low part of log2(e)), and
+// 2^(t + err) = 2^t * (1 + err*ln 2) to first order.  About 1.5 ulp; exact
+// 0 at -inf, +inf at +inf, NaN at NaN.  Used where routing needs many
+// exponentials (the softmax denominator).
+__device__ __forceinline__ float exp_fast(float x) {
+    constexpr float kLog2e = 1.44269502162933349609375f;   // log2(e) rounded to float
+    constexpr float kLog2eLo = 1.925963033500011e-8f;      // log2(e) - kLog2e
+    constexpr float kLn2 = 0.693147180559945309417f;
+    const float t = x * kLog2e;
+    const float err = __builtin_isfinite(t) ? fmaf(x, kLog2e, -t) + x * kLog2eLo : 0.f;
+    return __builtin_amdgcn_exp2f(t) * fmaf(err, kLn2, 1.0f);
+}
+
 __device__ __forceinline__ float silu_mul(float a, float b) {
     // activation kernel (elementwise.metal:8-17): a/(1+exp(-a))*b
     return a / (1.0f + __expf(-a)) * b;

@@ -35,7 +35,7 @@ __device__ __forceinline__ void route_wave_regs(const float *__restrict__ logits
     float den = 0.f;
 #pragma unroll
     for (int i = 0; i < R; i++)
-        if (lane + kWave * i < E) den += expf(v[i] - mx);
+        if (lane + kWave * i < E) den += exp_fast(v[i] - mx);
     den = wave_sum(den);
     // local best: strict > over ascending slots (= ascending j); NaN never wins
     float bv = -INFINITY;
@@ -75,7 +75,7 @@ __device__ __forceinline__ void route_wave_regs(const float *__restrict__ logits
         }
         // exhausted pool: id 0, score -inf (my_id/my_score keep their defaults)
     }
-    float wk = (uint32_t)lane < K ? expf(my_score - mx) / den : 0.f;
+    float wk = (uint32_t)lane < K ? exp_fast(my_score - mx) / den : 0.f;
     if (normalize) wk = wk / wave_sum(wk);
     if ((uint32_t)lane < K) {
         ids[lane] = my_id;
@@ -85,8 +85,8 @@ __device__ __forceinline__ void route_wave_regs(const float *__restrict__ logits
 
 // LDS scratch of one routing wave.
 struct RouteLds {
-    uint64_t mk[64];  // composite keys of the 64 lanes' local bests
-    uint64_t ck[64];  // composite keys of the surviving candidates
+    alignas(16) uint64_t mk[64];  // composite keys of the 64 lanes' local bests
+    alignas(16) uint64_t ck[64];  // composite keys of the surviving candidates
     uint32_t sj[64];  // selected ids by rank
     float sv[64];     // selected logits by rank
 };
@@ -140,11 +140,14 @@ __device__ __forceinline__ bool route_wave_rank(RouteLds *L, const float *__rest
     float den = 0.f;
 #pragma unroll
     for (int i = 0; i < R; i++)
-        if (lane + kWave * i < E) den += expf(v[i] - mx);
+        if (lane + kWave * i < E) den += exp_fast(v[i] - mx);
     wave_lds_sync();
     uint32_t rank = 0;
 #pragma unroll
-    for (int c = 0; c < kWave; c++) rank += L->mk[c] > my ? 1u : 0u;
+    for (int c = 0; c < kWave; c += 2) {
+        const ulonglong2 q = *reinterpret_cast<const ulonglong2 *>(&L->mk[c]);
+        rank += (q.x > my ? 1u : 0u) + (q.y > my ? 1u : 0u);
+    }
     den = wave_sum(den);
     const uint64_t tm = __ballot(rank == K - 1);
     uint32_t tval = 0;  // no lane at rank K-1: fewer than K lane bests -> keep all
@@ -163,12 +166,13 @@ __device__ __forceinline__ bool route_wave_rank(RouteLds *L, const float *__rest
 #pragma unroll
     for (int i = 0; i < R; i++)
         if (q[i]) L->ck[pos[i]] = ckey(v[i], lane + kWave * i);
+    if (total & 1u) L->ck[total] = 0ull;  // pad to whole pairs (odd total < 64); 0 ranks last
     wave_lds_sync();
     const uint64_t mine = (uint32_t)lane < total ? L->ck[lane] : 0ull;
     uint32_t r = 0;
     for (uint32_t c = 0; c < total; c += 2) {
-        const uint64_t c0 = L->ck[c], c1 = c + 1 < total ? L->ck[c + 1] : 0ull;
-        r += (c0 > mine ? 1u : 0u) + (c1 > mine ? 1u : 0u);
+        const ulonglong2 q = *reinterpret_cast<const ulonglong2 *>(&L->ck[c]);
+        r += (q.x > mine ? 1u : 0u) + (q.y > mine ? 1u : 0u);
     }
     if ((uint32_t)lane < total && r < K) {
         L->sj[r] = 0xffffu - (uint32_t)(mine & 0xffffu);
@@ -181,7 +185,7 @@ __device__ __forceinline__ bool route_wave_rank(RouteLds *L, const float *__rest
         score = L->sv[lane];
         id = L->sj[lane];
     }
-    float wk = (uint32_t)lane < K ? expf(score - mx) / den : 0.f;
+    float wk = (uint32_t)lane < K ? exp_fast(score - mx) / den : 0.f;
     if (normalize) wk = wk / wave_sum(wk);
     if ((uint32_t)lane < K) {
         ids[lane] = id;
@@ -205,7 +209,7 @@ __device__ __forceinline__ void route_wave_lds(float *vals, const float *__restr
     }
     const float mx = wave_max(m);
     float den = 0.f;
-    for (uint32_t j = lane; j < E; j += kWave) den += expf(vals[j] - mx);
+    for (uint32_t j = lane; j < E; j += kWave) den += exp_fast(vals[j] - mx);
     den = wave_sum(den);
     float selected = 0.f;
     for (uint32_t k = 0; k < K; k++) {
@@ -226,7 +230,7 @@ __device__ __forceinline__ void route_wave_lds(float *vals, const float *__restr
         const float score = none ? -INFINITY : M;
         if (!none && (best & (kWave - 1)) == (uint32_t)lane) vals[best] = -INFINITY;
         if (lane == 0) {
-            const float wk = expf(score - mx) / den;
+            const float wk = exp_fast(score - mx) / den;
             ids[k] = best;
             weights[k] = wk;
             selected += wk;
