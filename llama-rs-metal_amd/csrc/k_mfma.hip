@@ -270,9 +270,10 @@ __global__ __launch_bounds__(64) void to_bf16_kernel(const float *__restrict__ x
     }
 }
 
-// Tile list: M-tiles of kBM positions over every non-empty expert segment.
+// Tile list: M-tiles of `tm` positions over every non-empty expert segment.
 __global__ __launch_bounds__(64) void tile_schedule_kernel(const uint32_t *__restrict__ offsets,
-                                                           uint32_t E, uint32_t *__restrict__ tiles,
+                                                           uint32_t E, uint32_t tm,
+                                                           uint32_t *__restrict__ tiles,
                                                            uint32_t *__restrict__ ntiles) {
     const int lane = threadIdx.x;
     uint32_t base = 0;
@@ -281,7 +282,7 @@ __global__ __launch_bounds__(64) void tile_schedule_kernel(const uint32_t *__res
         uint32_t nt = 0, beg = 0;
         if (e < E) {
             beg = offsets[e];
-            nt = (offsets[e + 1] - beg + kBM - 1) / kBM;
+            nt = (offsets[e + 1] - beg + tm - 1) / tm;
         }
         // exclusive prefix of nt over the wave
         uint32_t incl = nt;
@@ -292,16 +293,17 @@ __global__ __launch_bounds__(64) void tile_schedule_kernel(const uint32_t *__res
         const uint32_t first = base + incl - nt;
         for (uint32_t i = 0; i < nt; i++) {
             tiles[2 * (first + i)] = e;
-            tiles[2 * (first + i) + 1] = beg + i * kBM;
+            tiles[2 * (first + i) + 1] = beg + i * tm;
         }
         base += __shfl(incl, 63, 64);
     }
     if (lane == 0) *ntiles = base;
 }
 
-// out[t, i] = sum_k y16[pos[t*K+k], i] (+ sh_out[t, i]/(1+exp(-sh_gate[t]))) (+ resid[t, i])
+// out[t, i] = sum_k w[t,k] * y16[pos[t*K+k], i] (+ sh_out[t, i]/(1+exp(-sh_gate[t]))) (+ resid[t, i])
 __global__ __launch_bounds__(256) void combine16_kernel(const uint16_t *__restrict__ y16,
                                                         const uint32_t *__restrict__ pos,
+                                                        const float *__restrict__ wts,
                                                         uint32_t K, const float *__restrict__ sh_out,
                                                         const float *__restrict__ sh_gate,
                                                         const float *__restrict__ resid,
@@ -309,10 +311,12 @@ __global__ __launch_bounds__(256) void combine16_kernel(const uint16_t *__restri
     const uint32_t t = blockIdx.y;
     for (uint32_t i = 2 * (blockIdx.x * 256 + threadIdx.x); i < h; i += 2 * 256 * gridDim.x) {
         float v0 = 0.f, v1 = 0.f;
+        // mix (elementwise.metal:47-57): sum over k ascending of w[k] * y_k
         for (uint32_t k = 0; k < K; k++) {
             const uint32_t w = reinterpret_cast<const uint32_t *>(y16 + (uint64_t)pos[(uint64_t)t * K + k] * h)[i / 2];
-            v0 += bf16_lo(w);
-            v1 += bf16_hi(w);
+            const float wk = wts[(uint64_t)t * K + k];
+            v0 += bf16_lo(w) * wk;
+            v1 += bf16_hi(w) * wk;
         }
         const uint64_t o = (uint64_t)t * h + i;
         if (sh_out) {
@@ -378,49 +382,24 @@ hipError_t launch_mfma_experts(Prof *p, hipStream_t s, const WDesc &gate, const 
                                uint32_t pairs, uint32_t *tiles, uint32_t *ntiles,
                                uint16_t *act16, uint16_t *y16) {
     const uint32_t E = gate.experts;
-    const uint32_t max_tiles = (pairs + kBM - 1) / kBM + E;
     prof_begin(p, s, "tile_schedule");
-    hipLaunchKernelGGL(tile_schedule_kernel, dim3(1), dim3(64), 0, s, offsets, E, tiles, ntiles);
+    hipLaunchKernelGGL(tile_schedule_kernel, dim3(1), dim3(64), 0, s, offsets, E, gemm_tile_rows(),
+                       tiles, ntiles);
     hipError_t e = hipGetLastError();
     prof_end(p, s);
     if (e != hipSuccess) return e;
-    MfmaArgs g{};
-    g.w = gate;
-    g.w2 = up;
-    g.a_rows = xb16;
-    g.perm = perm;
-    g.offsets = offsets;
-    g.tiles = tiles;
-    g.ntiles = ntiles;
-    g.out_bf16 = act16;
-    g.k = k;
-    prof_begin(p, s, "mfma_gateup");
-    e = dispatch_kind(gate, MfmaLaunch<MODE_GATEUP>{s, g, dim3(max_tiles, (gate.out + kBN / 2 - 1) / (kBN / 2))});
-    prof_end(p, s);
+    e = launch_grouped_gemm(p, s, 0, gate, up, xb16, perm, offsets, tiles, ntiles, nullptr, k, act16);
     if (e != hipSuccess) return e;
-    MfmaArgs d{};
-    d.w = down;
-    d.a_rows = act16;
-    d.perm = perm;
-    d.offsets = offsets;
-    d.tiles = tiles;
-    d.ntiles = ntiles;
-    d.route_w = route_w;
-    d.out_bf16 = y16;
-    d.k = k;
-    prof_begin(p, s, "mfma_down");
-    e = dispatch_kind(down, MfmaLaunch<MODE_DOWN>{s, d, dim3(max_tiles, (down.out + kBN - 1) / kBN)});
-    prof_end(p, s);
-    return e;
+    return launch_grouped_gemm(p, s, 1, down, down, act16, perm, offsets, tiles, ntiles, route_w, k, y16);
 }
 
 hipError_t launch_combine16(Prof *p, hipStream_t s, const uint16_t *y16, const uint32_t *pos,
-                            uint32_t k, const float *sh_out, const float *sh_gate,
+                            const float *wts, uint32_t k, const float *sh_out, const float *sh_gate,
                             const float *resid, float *out, uint32_t tokens, uint32_t h) {
     prof_begin(p, s, "combine16");
     dim3 grid((h / 2 + 255) / 256, tokens);
-    hipLaunchKernelGGL(combine16_kernel, grid, dim3(256), 0, s, y16, pos, k, sh_out, sh_gate, resid,
-                       out, h);
+    hipLaunchKernelGGL(combine16_kernel, grid, dim3(256), 0, s, y16, pos, wts, k, sh_out, sh_gate,
+                       resid, out, h);
     hipError_t e = hipGetLastError();
     prof_end(p, s);
     return e;

@@ -236,7 +236,7 @@ moe_status run_mfma(moe_gpu *g, const moe_block_weights *w, const Dims &d, const
         so = sout;
         sgv = sgt;
     }
-    TRY(launch_combine16(p, s, y16, pos, K, so, sgv, io->residual ? xraw : nullptr, out, (uint32_t)T,
+    TRY(launch_combine16(p, s, y16, pos, wts, K, so, sgv, io->residual ? xraw : nullptr, out, (uint32_t)T,
                          (uint32_t)d.h));
     return MOE_OK;
 }
