@@ -40,27 +40,67 @@ typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kWM = 2;                   // waves along M (64 rows each); 2 waves along N
-constexpr int kTM = 64 * kWM;            // pairs per work item
-constexpr int kTN = 128;                 // weight rows per tile
+// Block layout: kWM x kWN waves, each owning kMT x kNT MFMA tiles of 32x32.
+constexpr int kWM = 2, kWN = 2;          // waves along M / along N
+constexpr int kMT = 2, kNT = 2;          // 32x32 tiles per wave along M / along N
+constexpr int kTM = 32 * kMT * kWM;      // pairs per work item
+constexpr int kTN = 32 * kNT * kWN;      // weight rows per tile
 constexpr int kTK = 64;                  // K per step
-constexpr int kRowBytes = kTK * 2 + 16;  // LDS row: 64 bf16 + 16-byte pad (bank spread)
+constexpr int kRowBytes = kTK * 2 + 16;  // LDS row: kTK bf16 + 16-byte pad (bank spread)
 constexpr int kATile = kTM * kRowBytes;  // one A stage
 constexpr int kBTile = kTN * kRowBytes;  // one B stage
 constexpr int kLdsBytes = 2 * kATile + 2 * kBTile;  // A and B, double-buffered
-constexpr int kThreads = 64 * kWM * 2;   // waves: kWM along M x 2 along N, 64x64 each
-constexpr int kBlocksPerCu = kWM == 2 ? 2 : 1;
+constexpr int kThreads = 64 * kWM * kWN;
+constexpr int kMaxBlocksPerCu = 2;      // occupancy target (LDS and VGPRs allowing)
+constexpr int kBlocksPerCu = kLdsBytes * kMaxBlocksPerCu <= 160 * 1024 ? kMaxBlocksPerCu
+                             : kLdsBytes * 2 <= 160 * 1024            ? 2 : 1;
 constexpr int kBVals = kTN * kTK / kThreads;  // weight values one thread dequantises per step
-constexpr int kARowsPerPass = kThreads / 8;   // A rows one pass of 16-byte loads covers
+constexpr int kAChunksPerRow = kTK * 2 / 16;  // 16-byte chunks of one A row per step
+constexpr int kAChunks = kTM * kAChunksPerRow / kThreads;  // A chunks one thread stages per step
+constexpr int kARowsPerPass = kThreads / kAChunksPerRow;   // A rows one pass covers
 constexpr int kXcds = 8;
+constexpr bool kInterleave = false;  // spread dequant VALU and LDS reads between the MFMAs
 
 enum { GATEUP = 1, DOWN = 2 };
-static_assert((kWM == 2 || kWM == 4) && kTN == 128 && (kBVals == 16 || kBVals == 32),
-              "wave layout kWM x 2 over 64x64 sub-tiles");
+static_assert(kNT % 2 == 0, "gate/up columns pair up inside a wave");
+static_assert(kBVals == 16 || kBVals == 32 || kBVals == 64, "whole words of codes per thread");
+static_assert(kTM * kAChunksPerRow % kThreads == 0, "whole A chunks per thread");
+static_assert(kTK == 32 || kTK == 64, "K step");
 
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
     const f32x2 v = {a, b};
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+// Byte N of v as float: one v_cvt_f32_ubyteN (the compiler otherwise splits
+// masked nibble extractions into a bit-field extract plus a conversion).
+template <int N>
+__device__ __forceinline__ float cvt_ubyte(uint32_t v) {
+    float r;
+    if constexpr (N == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
+    else if constexpr (N == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
+    else if constexpr (N == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
+    else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+
+// The codes of one packed word (low bits first) as floats: the word is split
+// into byte-aligned code planes (one mask per plane), then each code converts
+// with one instruction.
+template <int BITS>
+__device__ __forceinline__ void codes_f32(uint32_t w, float *c) {
+    constexpr int P = 32 / BITS;        // codes per word
+    constexpr int PLANES = 8 / BITS;    // codes per byte
+    constexpr uint32_t kMask = BITS == 8 ? 0xffffffffu : BITS == 4 ? 0x0f0f0f0fu : 0x03030303u;
+#pragma unroll
+    for (int pl = 0; pl < PLANES; pl++) {
+        const uint32_t v = (w >> (BITS * pl)) & kMask;  // code pl of every byte
+        c[pl] = cvt_ubyte<0>(v);
+        c[pl + PLANES] = cvt_ubyte<1>(v);
+        c[pl + 2 * PLANES] = cvt_ubyte<2>(v);
+        c[pl + 3 * PLANES] = cvt_ubyte<3>(v);
+    }
+    static_assert(P == 4 * PLANES, "four bytes per word");
 }
 
 struct Args {
@@ -138,7 +178,7 @@ struct BStage {
 #pragma unroll
             for (int i = 0; i < NW; i++) {
                 float c[P];
-                unpack_word<BITS>(w[i], c);
+                codes_f32<BITS>(w[i], c);
 #pragma unroll
                 for (int j = 0; j < P; j += 2)
                     o[(i * P + j) / 2] = pack_bf16(fmaf(c[j], sf, bf), fmaf(c[j + 1], sf, bf));
@@ -176,7 +216,7 @@ template <int MODE, int BITS, int T>
 __global__ __launch_bounds__(kThreads, kBlocksPerCu) void grouped_gemm_kernel(Args a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int wm = wv % kWM, wn = wv / kWM;  // wave's 64-row group and 64-column group
+    const int wm = wv % kWM, wn = wv / kWM;  // wave's row group and column group
     const uint32_t in = a.w.in, out = a.w.out;
     const uint32_t nk = in / kTK;
     // ---- this block's share of the work items ----
@@ -184,8 +224,9 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void grouped_gemm_kernel(Ar
     const uint32_t xcd = blockIdx.x % kXcds, q = blockIdx.x / kXcds, nq = gridDim.x / kXcds;
     const uint32_t per_xcd = (items + kXcds - 1) / kXcds;
     const uint32_t lo = xcd * per_xcd, hi = min(items, lo + per_xcd);
-    // A staging: thread -> rows tid/8 + kARowsPerPass*i, 16-byte chunk tid%8 of the K slice
-    const int ac = tid & 7, ar = tid >> 3;
+    // A staging: thread -> rows tid/kAChunksPerRow + kARowsPerPass*i, 16-byte chunk
+    // tid%kAChunksPerRow of the K slice
+    const int ac = tid % kAChunksPerRow, ar = tid / kAChunksPerRow;
     // B staging: thread -> tile row, kBVals values at kBVals*(quarter)
     constexpr int kBPerRow = kTK / kBVals;
     const int br = tid / kBPerRow, bq = tid % kBPerRow;
@@ -194,15 +235,16 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void grouped_gemm_kernel(Ar
         const uint32_t mt = item / a.n_tiles_n, nt = item % a.n_tiles_n;
         const uint32_t e = a.tiles[2 * mt], m0 = a.tiles[2 * mt + 1];
         const uint32_t seg_end = a.offsets[e + 1];
-        // with 4 waves along M the second 128-row half may be empty: its waves
-        // then only load and dequantise
-        const bool half_live = m0 + 64 * (uint32_t)(wm & ~1) < seg_end;
+        // a wave whose rows all lie past the segment only loads and
+        // dequantises (with one or two 64-row wave groups along M the first
+        // rows are always live: no branch)
+        const bool half_live = kMT * kWM <= 2 || m0 + 32 * kMT * (uint32_t)wm < seg_end;
         // A rows of this thread.  Rows past the segment read the segment's
         // first row instead: a C row depends only on its own A row, and those
         // rows are never stored.
-        const uint16_t *asrc[4];
+        const uint16_t *asrc[kAChunks];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < kAChunks; i++) {
             uint32_t pos = m0 + ar + kARowsPerPass * i;
             if (pos >= seg_end) pos = m0;
             const uint64_t src = MODE == GATEUP ? a.perm[pos] / a.k : pos;
@@ -217,7 +259,7 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void grouped_gemm_kernel(Ar
             if constexpr (MODE == GATEUP) {
                 const int q32 = br >> 5;  // 32-row groups alternate gate / up
                 j = nt * (kTN / 2) + (q32 >> 1) * 32 + (br & 31);
-                second = (q32 & 1) != 0;
+                second = (q32 & 1) != 0;  // tile rows 32(2i+1).. are up rows
             } else {
                 j = nt * kTN + br;
             }
@@ -227,28 +269,28 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void grouped_gemm_kernel(Ar
                           : make_bsrc<BITS, T>(a.w, grow, kBVals * bq);
         }
 
-        f32x16 acc[2][2];
+        f32x16 acc[kMT][kNT];
 #pragma unroll
-        for (int s = 0; s < 2; s++)
+        for (int s = 0; s < kMT; s++)
 #pragma unroll
-            for (int t = 0; t < 2; t++)
+            for (int t = 0; t < kNT; t++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) acc[s][t][r] = 0.f;
 
         // Two register stages: the global loads for step kb + 2 are issued in
         // iteration kb, stored to LDS in iteration kb + 1, used in kb + 2.
-        u32x4 av[2][4];
+        u32x4 av[2][kAChunks];
         BStage<BITS, T> bs[2];
         auto load_step = [&](int st, uint32_t kb) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) av[st][i] = *reinterpret_cast<const u32x4 *>(asrc[i] + kb * kTK);
+            for (int i = 0; i < kAChunks; i++) av[st][i] = *reinterpret_cast<const u32x4 *>(asrc[i] + kb * kTK);
             bs[st].load(bsrc, kb);
         };
         auto store_step = [&](int st, int buf) {
             uint8_t *At = lds + buf * kATile;
             uint8_t *Bt = lds + 2 * kATile + buf * kBTile;
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int i = 0; i < kAChunks; i++)
                 *reinterpret_cast<u32x4 *>(At + (ar + kARowsPerPass * i) * kRowBytes + 16 * ac) = av[st][i];
             uint32_t o[kBVals / 2];
             bs[st].to_bf16(o);
@@ -271,23 +313,35 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void grouped_gemm_kernel(Ar
                 const uint8_t *Bt = lds + 2 * kATile + ST * kBTile;
                 const int h = lane >> 5;
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int koff = (32 * h + 8 * j) * 2;
-                    bf16x8 af[2], bf[2];
+                for (int j = 0; j < kTK / 16; j++) {
+                    const int koff = ((kTK / 2) * h + 8 * j) * 2;
+                    bf16x8 af[kMT], bf[kNT];
 #pragma unroll
-                    for (int s = 0; s < 2; s++)
-                        af[s] = *reinterpret_cast<const bf16x8 *>(At + (64 * wm + 32 * s + (lane & 31)) * kRowBytes + koff);
+                    for (int s = 0; s < kMT; s++)
+                        af[s] = *reinterpret_cast<const bf16x8 *>(At + (32 * (kMT * wm + s) + (lane & 31)) * kRowBytes + koff);
 #pragma unroll
-                    for (int t = 0; t < 2; t++)
-                        bf[t] = *reinterpret_cast<const bf16x8 *>(Bt + (64 * wn + 32 * t + (lane & 31)) * kRowBytes + koff);
+                    for (int t = 0; t < kNT; t++)
+                        bf[t] = *reinterpret_cast<const bf16x8 *>(Bt + (32 * (kNT * wn + t) + (lane & 31)) * kRowBytes + koff);
 #pragma unroll
-                    for (int s = 0; s < 2; s++)
+                    for (int s = 0; s < kMT; s++)
 #pragma unroll
-                        for (int t = 0; t < 2; t++)
+                        for (int t = 0; t < kNT; t++)
                             acc[s][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s], bf[t], acc[s][t], 0, 0, 0);
                 }
             }
             store_step(ST ^ 1, ST ^ 1);  // may interleave with the MFMAs above
+            if constexpr (kInterleave) {
+                // per MFMA: one fragment read and a share of the dequantisation,
+                // so the VALU and LDS work issues in the MFMAs' shadow
+                constexpr int kMfmas = kMT * kNT * (kTK / 16);
+#pragma unroll
+                for (int i = 0; i < kMfmas; i++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+                    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
+                }
+                __builtin_amdgcn_sched_group_barrier(0x200, 16, 0);    // DS writes
+            }
             __syncthreads();
         };
         load_step(0, 0);
@@ -298,27 +352,33 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void grouped_gemm_kernel(Ar
             iter(kb, std::integral_constant<int, 0>{});
             iter(kb + 1, std::integral_constant<int, 1>{});
         }
-        // ---- epilogue: acc[s][t][r] = C[64wm+32s+8(r/4)+4(lane/32)+(r%4)][64wn+32t+lane%32] ----
+        // ---- epilogue: acc[s][t][r] = C[32(kMT wm + s) + 8(r/4) + 4(lane/32) + (r%4)]
+        //                             [32(kNT wn + t) + lane%32]
         if (!half_live) continue;
 #pragma unroll
-        for (int s = 0; s < 2; s++) {
+        for (int s = 0; s < kMT; s++) {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const uint32_t pos = m0 + 64 * wm + 32 * s + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                const uint32_t pos = m0 + 32 * (kMT * wm + s) + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (pos >= seg_end) continue;
                 if constexpr (MODE == GATEUP) {
-                    const uint32_t j = nt * (kTN / 2) + 32 * wn + (lane & 31);
-                    if (j < out) {
-                        // activation (elementwise.metal:8-17) with the base-2 exponential
-                        // and a hardware reciprocal: the result is rounded to bf16
-                        const float g = acc[s][0][r], u = acc[s][1][r];
-                        const float act = g * __builtin_amdgcn_rcpf(1.0f + exp_fast(-g)) * u;
-                        a.out[(uint64_t)pos * out + j] = (uint16_t)(pack_bf16(act, 0.f) & 0xffffu);
+                    // B rows 32(2i) .. are gate columns, 32(2i+1) .. the same up columns
+#pragma unroll
+                    for (int t = 0; t < kNT; t += 2) {
+                        const uint32_t j = nt * (kTN / 2) + 32 * ((kNT * wn + t) / 2) + (lane & 31);
+                        if (j < out) {
+                            // activation (elementwise.metal:8-17) with the base-2
+                            // exponential and a hardware reciprocal (the result is
+                            // rounded to bf16)
+                            const float g = acc[s][t][r], u = acc[s][t + 1][r];
+                            const float act = g * __builtin_amdgcn_rcpf(1.0f + exp_fast(-g)) * u;
+                            a.out[(uint64_t)pos * out + j] = (uint16_t)(pack_bf16(act, 0.f) & 0xffffu);
+                        }
                     }
                 } else {
 #pragma unroll
-                    for (int t = 0; t < 2; t++) {
-                        const uint32_t n = nt * kTN + 64 * wn + 32 * t + (lane & 31);
+                    for (int t = 0; t < kNT; t++) {
+                        const uint32_t n = nt * kTN + 32 * (kNT * wn + t) + (lane & 31);
                         if (n < out)
                             a.out[(uint64_t)pos * out + n] = (uint16_t)(pack_bf16(acc[s][t][r], 0.f) & 0xffffu);
                     }
