@@ -40,6 +40,7 @@ ROUTER_BYTES = H * E * 4 + H * 4                                    # F32 router
 GATEUP_BYTES = K * 2 * MAT_BYTES + 2 * MAT_BYTES                    # decode_gateup per launch (routed + shared gate/up)
 HBM_PEAK = 8.0e12
 CHUNK = 64       # steps per captured graph
+HOLD_US = 40000  # stream hold before a profiled batch (covers its host enqueue)
 LAYERS = 8       # distinct weight sets rotated
 
 
@@ -109,6 +110,7 @@ def bench_prefill(gpu, iters=10):
     gpu.profile_reset()
     gpu.profile(True)
     with gpu.batch() as b:
+        b.hold(HOLD_US)  # every launch queued before the GPU starts: events time GPU work only
         b.moe_block(bw, x, out, P_T, ws, logit_bias=bias, ids_out=ids)
     prof = gpu.profile_read()
     gpu.profile(False)
@@ -118,7 +120,7 @@ def bench_prefill(gpu, iters=10):
     t = b.seconds / iters
     counts = np.bincount(gpu.read_u32(ids), minlength=P_E)
     k_us = {k: round(v[1] / v[0] * 1e6, 2) for k, v in prof.items()}
-    expert_s = sum(v[1] / v[0] for k, v in prof.items() if k in ("mfma_gateup", "mfma_down"))
+    expert_s = sum(v[1] / v[0] for k, v in prof.items() if k in ("gemm_gateup", "gemm_down"))
     for buf in (x, out, ws, bias, ids):
         gpu.release(buf)
     return {
@@ -239,13 +241,20 @@ def main():
         o = outs.view(j * H, H)
         b.moe_block(layers[j % LAYERS], x, o, 1, ws)
 
-    # per-kernel durations (hipEvents around each launch, eager)
+    # per-kernel durations: hipEvents around each launch on the library's
+    # stream, with the stream held until all CHUNK steps are enqueued so that
+    # the events bracket GPU execution and not host enqueue gaps
     gpu.profile_reset()
     gpu.profile(True)
     with gpu.batch() as b:
+        b.hold(HOLD_US)
+        t_enq = time.perf_counter()
         for j in range(CHUNK):
             issue(b, j)
+        t_enq = time.perf_counter() - t_enq
     prof = gpu.profile_read()
+    if t_enq * 1e6 > HOLD_US:
+        log(f"[bench] warning: enqueue took {t_enq * 1e3:.1f} ms, longer than the hold")
     gpu.profile(False)
     kernels = {k: v[1] / v[0] for k, v in prof.items()}
     log("[bench] kernel averages (us): " + ", ".join(f"{k} {v * 1e6:.2f}" for k, v in kernels.items()))

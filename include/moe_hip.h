@@ -235,6 +235,12 @@ moe_status moe_profile_count(moe_gpu *gpu, uint32_t *n);
 moe_status moe_profile_get(moe_gpu *gpu, uint32_t index, char *name, size_t cap,
                            uint64_t *launches, double *seconds);
 moe_status moe_profile_reset(moe_gpu *gpu);
+/* Inside an open batch (not a capture): occupy the stream for `microseconds`
+ * (<= 100000) so that the launches enqueued next are all queued before the
+ * GPU reaches them and profiled durations exclude host enqueue gaps.  No
+ * counterpart in the reference (Metal command buffers are committed whole);
+ * a measurement aid for moe_profile_*. */
+moe_status moe_profile_hold(moe_gpu *gpu, uint32_t microseconds);
 
 /* Stream capture of a batch into a replayable HIP graph (launch-bound decode
  * loops).  moe_graph_begin opens a batch in capture mode; moe_graph_end

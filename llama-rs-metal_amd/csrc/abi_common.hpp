@@ -28,7 +28,6 @@ struct Prof {
     };
     std::vector<Pending> pending;
     std::vector<hipEvent_t> pool;
-    int open = -1;  // index into pending of the launch being bracketed
 };
 void prof_collect(Prof *p, hipStream_t s);
 

@@ -349,16 +349,23 @@ __global__ __launch_bounds__(64) void decode_gateup_kernel(DecodeKArgs a) {
         }
         return;
     }
-    // route (sampling.metal:1-36), exact, redundantly per wave
-    route_one_wave(&route_lds, route_vals, a.logits, a.E, a.k, (int)a.normalize, s_ids, s_w, lane);
-    __syncthreads();
-    if (wave_id == 0 && lane < a.k) {
-        a.ids[lane] = s_ids[lane];
-        a.weights[lane] = s_w[lane];
-    }
+    // route (sampling.metal:1-36), exact, redundantly per wave: wave 0 derives
+    // the ids and weights the down kernel reads, every other wave only the id
+    // of its own selection pass kk
     const uint32_t kk = wave_id / a.n_gate_waves_per_expert;
     const uint32_t item = wave_id % a.n_gate_waves_per_expert;
-    const uint32_t e = s_ids[kk];  // < E by construction of route
+    uint32_t e;  // < E by construction of route
+    if (wave_id == 0) {
+        route_one_wave(&route_lds, route_vals, a.logits, a.E, a.k, (int)a.normalize, s_ids, s_w, lane);
+        __syncthreads();
+        if (lane < a.k) {
+            a.ids[lane] = s_ids[lane];
+            a.weights[lane] = s_w[lane];
+        }
+        e = s_ids[0];
+    } else {
+        e = route_one_id(&route_lds, route_vals, a.logits, a.E, a.k, kk, lane);
+    }
     uint64_t rows[kGateFR];
     bool ok[kGateFR];
 #pragma unroll
@@ -531,27 +538,19 @@ bool decode_supported(const DecodeArgs &a) {
 template <int BITS, int ST>
 static hipError_t launch_decode_t(Prof *p, hipStream_t s, const DecodeKArgs &k) {
     const uint32_t pre_waves = k.n_router_waves + (k.has_shared ? 1 : 0);
-    prof_begin(p, s, "decode_pre");
-    hipLaunchKernelGGL((decode_pre_kernel<ST>), dim3(pre_waves), dim3(64), 0, s, k);
-    hipError_t e = hipGetLastError();
-    prof_end(p, s);
+    hipError_t e = launch_kernel(p, "decode_pre", decode_pre_kernel<ST>, dim3(pre_waves), dim3(64), 0,
+                                 s, k);
     if (e != hipSuccess) return e;
     const uint32_t gate_waves = k.k * k.n_gate_waves_per_expert + (k.has_shared ? k.n_shared_waves : 0);
     const size_t lds = k.E > 1024 ? (size_t)k.E * sizeof(float) : 0;
-    prof_begin(p, s, "decode_gateup");
-    hipLaunchKernelGGL((decode_gateup_kernel<BITS, ST>), dim3(gate_waves), dim3(64), lds, s, k);
-    e = hipGetLastError();
-    prof_end(p, s);
+    e = launch_kernel(p, "decode_gateup", decode_gateup_kernel<BITS, ST>, dim3(gate_waves), dim3(64),
+                      lds, s, k);
     if (e != hipSuccess) return e;
     const uint32_t rows_per_block = (64u / k.lpr_f) * kDownFR;
     const uint32_t n_exp = k.k + (k.has_shared ? 1u : 0u);
     const uint32_t nw = n_exp < (uint32_t)kDownMaxWaves ? n_exp : (uint32_t)kDownMaxWaves;
-    prof_begin(p, s, "decode_down");
-    hipLaunchKernelGGL((decode_down_kernel<BITS, ST>), dim3((k.h + rows_per_block - 1) / rows_per_block),
-                       dim3(64 * nw), 0, s, k);
-    e = hipGetLastError();
-    prof_end(p, s);
-    return e;
+    return launch_kernel(p, "decode_down", decode_down_kernel<BITS, ST>,
+                         dim3((k.h + rows_per_block - 1) / rows_per_block), dim3(64 * nw), 0, s, k);
 }
 
 hipError_t launch_decode(Prof *p, hipStream_t s, const DecodeArgs &a) {

@@ -88,12 +88,8 @@ __global__ void combine_kernel(const float *__restrict__ yexp, const uint32_t *_
     }
 }
 
-#define EW_LAUNCH(name, kern, n, ...)                                        \
-    prof_begin(p, s, name);                                                   \
-    hipLaunchKernelGGL(kern, ew_grid(n), dim3(kEw), 0, s, __VA_ARGS__);       \
-    hipError_t e = hipGetLastError();                                          \
-    prof_end(p, s);                                                            \
-    return e;
+#define EW_LAUNCH(name, kern, n, ...) \
+    return launch_kernel(p, name, kern, ew_grid(n), dim3(kEw), 0, s, __VA_ARGS__);
 
 hipError_t launch_swiglu(Prof *p, hipStream_t s, const float *a, const float *b, float *y,
                          uint64_t n) {
@@ -117,28 +113,32 @@ hipError_t launch_copy(Prof *p, hipStream_t s, const float *src, float *dst, uin
 
 hipError_t launch_norm(Prof *p, hipStream_t s, const float *x, const void *w, uint32_t wtype,
                        float *y, uint32_t heads, uint32_t n, uint32_t stride, float eps) {
-    prof_begin(p, s, "norm");
-    if (wtype == 0)
-        hipLaunchKernelGGL(norm_kernel<0>, dim3(heads), dim3(64), 0, s, x, w, y, n, stride, eps);
-    else if (wtype == 1)
-        hipLaunchKernelGGL(norm_kernel<1>, dim3(heads), dim3(64), 0, s, x, w, y, n, stride, eps);
-    else
-        hipLaunchKernelGGL(norm_kernel<30>, dim3(heads), dim3(64), 0, s, x, w, y, n, stride, eps);
-    hipError_t e = hipGetLastError();
-    prof_end(p, s);
-    return e;
+    auto kern = wtype == 0 ? norm_kernel<0> : wtype == 1 ? norm_kernel<1> : norm_kernel<30>;
+    return launch_kernel(p, "norm", kern, dim3(heads), dim3(64), 0, s, x, w, y, n, stride, eps);
 }
 
 hipError_t launch_combine(Prof *p, hipStream_t s, const float *yexp, const uint32_t *pos,
                           const float *w, uint32_t k, const float *sh_out, const float *sh_gate,
                           const float *resid, float *out, uint32_t tokens, uint32_t h) {
-    prof_begin(p, s, "combine");
     dim3 grid((h + kEw - 1) / kEw, tokens);
-    hipLaunchKernelGGL(combine_kernel, grid, dim3(kEw), 0, s, yexp, pos, w, k, sh_out, sh_gate,
-                       resid, out, tokens, h);
-    hipError_t e = hipGetLastError();
-    prof_end(p, s);
-    return e;
+    return launch_kernel(p, "combine", combine_kernel, grid, dim3(kEw), 0, s, yexp, pos, w, k,
+                         sh_out, sh_gate, resid, out, tokens, h);
+}
+
+// Keeps the stream busy for `ticks` of the 100 MHz constant clock: the
+// launches queued behind it are all enqueued before the GPU reaches them, so
+// per-launch events measure GPU time and not host enqueue gaps.  Bounded
+// twice: by the clock and by an iteration count (each s_sleep 127 lasts
+// 127*64 shader cycles, over 3 us at 2.4 GHz).
+__global__ __launch_bounds__(64) void hold_kernel(uint64_t ticks, uint32_t max_iters) {
+    const uint64_t t0 = wall_clock64();
+    for (uint32_t i = 0; i < max_iters && wall_clock64() - t0 < ticks; i++)
+        __builtin_amdgcn_s_sleep(127);
+}
+
+hipError_t launch_hold(hipStream_t s, uint32_t microseconds) {
+    return launch_kernel(nullptr, "hold", hold_kernel, dim3(1), dim3(64), 0, s,
+                         (uint64_t)microseconds * 100u, microseconds / 2u + 2u);
 }
 
 }  // namespace moehip

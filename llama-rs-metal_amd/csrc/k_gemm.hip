@@ -390,14 +390,15 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void grouped_gemm_kernel(Ar
 
 template <int MODE>
 struct Launch {
+    Prof *p;
     hipStream_t s;
     const Args &a;
     uint32_t blocks;
     template <int BITS, int T>
     hipError_t operator()() {
-        hipLaunchKernelGGL((grouped_gemm_kernel<MODE, BITS, T>), dim3(blocks), dim3(kThreads), kLdsBytes,
-                           s, a);
-        return hipGetLastError();
+        return launch_kernel(p, MODE == DOWN ? "gemm_down" : "gemm_gateup",
+                             grouped_gemm_kernel<MODE, BITS, T>, dim3(blocks), dim3(kThreads),
+                             kLdsBytes, s, a);
     }
 };
 
@@ -450,15 +451,12 @@ hipError_t launch_grouped_gemm(Prof *p, hipStream_t s, int down, const WDesc &w,
     if (down) {
         a.n_tiles_n = (w.out + gemm::kTN - 1) / gemm::kTN;
         if ((e = dispatch_kind(w, SetLds<gemm::DOWN>{})) != hipSuccess) return e;
-        prof_begin(p, s, "gemm_down");
-        e = dispatch_kind(w, gemm::Launch<gemm::DOWN>{s, a, blocks});
+        e = dispatch_kind(w, gemm::Launch<gemm::DOWN>{p, s, a, blocks});
     } else {
         a.n_tiles_n = (w.out + gemm::kTN / 2 - 1) / (gemm::kTN / 2);
         if ((e = dispatch_kind(w, SetLds<gemm::GATEUP>{})) != hipSuccess) return e;
-        prof_begin(p, s, "gemm_gateup");
-        e = dispatch_kind(w, gemm::Launch<gemm::GATEUP>{s, a, blocks});
+        e = dispatch_kind(w, gemm::Launch<gemm::GATEUP>{p, s, a, blocks});
     }
-    prof_end(p, s);
     return e;
 }
 

@@ -28,6 +28,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(WDesc w, const float *__restr
 }
 
 struct GemvLaunch {
+    Prof *p;
     hipStream_t s;
     const WDesc &w;
     const float *x;
@@ -39,8 +40,8 @@ struct GemvLaunch {
     template <int BITS, int T>
     hipError_t operator()() {
         dim3 grid((w.out + 3) / 4, nsel, tokens);
-        hipLaunchKernelGGL((gemv_kernel<BITS, T>), grid, dim3(256), 0, s, w, x, xs, ids, y, tokens);
-        return hipGetLastError();
+        return launch_kernel(p, "gemv_generic", gemv_kernel<BITS, T>, grid, dim3(256), 0, s, w, x, xs,
+                             ids, y, tokens);
     }
 };
 
@@ -48,19 +49,17 @@ hipError_t launch_gemv(Prof *p, hipStream_t s, const WDesc &w, const float *x,
                        uint64_t x_sel_stride, const uint32_t *ids, uint32_t nsel, float *y,
                        uint32_t tokens) {
     if (w.out == 0 || nsel == 0 || tokens == 0) return hipSuccess;
-    prof_begin(p, s, "gemv_generic");
     hipError_t e = hipSuccess;
     if (nsel == 1) {
         // grid.z is limited to 65535: split long token runs (matmul only).
         for (uint32_t t0 = 0; t0 < tokens && e == hipSuccess; t0 += 65535u) {
             const uint32_t n = tokens - t0 < 65535u ? tokens - t0 : 65535u;
-            e = dispatch_kind(w, GemvLaunch{s, w, x + (uint64_t)t0 * w.in, x_sel_stride, ids, 1,
+            e = dispatch_kind(w, GemvLaunch{p, s, w, x + (uint64_t)t0 * w.in, x_sel_stride, ids, 1,
                                             y + (uint64_t)t0 * w.out, n});
         }
     } else {
-        e = dispatch_kind(w, GemvLaunch{s, w, x, x_sel_stride, ids, nsel, y, tokens});
+        e = dispatch_kind(w, GemvLaunch{p, s, w, x, x_sel_stride, ids, nsel, y, tokens});
     }
-    prof_end(p, s);
     return e;
 }
 

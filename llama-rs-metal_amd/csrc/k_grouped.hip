@@ -49,6 +49,7 @@ __global__ __launch_bounds__(256) void grouped_down_kernel(WDesc d, const float 
 }
 
 struct GateUpLaunch {
+    Prof *p;
     hipStream_t s;
     const WDesc &g, &u;
     const float *x;
@@ -58,13 +59,13 @@ struct GateUpLaunch {
     template <int BITS, int T>
     hipError_t operator()() {
         dim3 grid(E, (g.out + 3) / 4);
-        hipLaunchKernelGGL((grouped_gateup_kernel<BITS, T>), grid, dim3(256), 0, s, g, u, x,
-                           offsets, perm, K, act);
-        return hipGetLastError();
+        return launch_kernel(p, "grouped_gateup_valu", grouped_gateup_kernel<BITS, T>, grid,
+                             dim3(256), 0, s, g, u, x, offsets, perm, K, act);
     }
 };
 
 struct DownLaunch {
+    Prof *p;
     hipStream_t s;
     const WDesc &d;
     const float *act;
@@ -74,29 +75,22 @@ struct DownLaunch {
     template <int BITS, int T>
     hipError_t operator()() {
         dim3 grid(E, (d.out + 3) / 4);
-        hipLaunchKernelGGL((grouped_down_kernel<BITS, T>), grid, dim3(256), 0, s, d, act, offsets,
-                           yexp);
-        return hipGetLastError();
+        return launch_kernel(p, "grouped_down_valu", grouped_down_kernel<BITS, T>, grid, dim3(256),
+                             0, s, d, act, offsets, yexp);
     }
 };
 
 hipError_t launch_grouped_gateup(Prof *p, hipStream_t s, const WDesc &gate, const WDesc &up,
                                  const float *x, const uint32_t *offsets, const uint32_t *perm,
                                  uint32_t k, uint32_t experts, float *act) {
-    prof_begin(p, s, "grouped_gateup_valu");
-    hipError_t e = dispatch_kind(gate, GateUpLaunch{s, gate, up, x, offsets, perm, k, experts, act});
-    prof_end(p, s);
-    return e;
+    return dispatch_kind(gate, GateUpLaunch{p, s, gate, up, x, offsets, perm, k, experts, act});
 }
 
 hipError_t launch_grouped_down(Prof *p, hipStream_t s, const WDesc &down, const float *act,
                                const uint32_t *offsets, uint32_t experts, uint32_t pairs,
                                float *yexp) {
     (void)pairs;
-    prof_begin(p, s, "grouped_down_valu");
-    hipError_t e = dispatch_kind(down, DownLaunch{s, down, act, offsets, experts, yexp});
-    prof_end(p, s);
-    return e;
+    return dispatch_kind(down, DownLaunch{p, s, down, act, offsets, experts, yexp});
 }
 
 }  // namespace moehip

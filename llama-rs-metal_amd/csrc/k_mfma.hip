@@ -342,23 +342,21 @@ bool mfma_supported(const WDesc &w) {
 
 template <int MODE>
 struct MfmaLaunch {
+    Prof *p;
+    const char *name;
     hipStream_t s;
     const MfmaArgs &a;
     dim3 grid;
     template <int BITS, int T>
     hipError_t operator()() {
-        hipLaunchKernelGGL((grouped_mfma_kernel<MODE, BITS, T>), grid, dim3(256), 0, s, a);
-        return hipGetLastError();
+        return launch_kernel(p, name, grouped_mfma_kernel<MODE, BITS, T>, grid, dim3(256), 0, s, a);
     }
 };
 
 hipError_t launch_to_bf16(Prof *p, hipStream_t s, const float *x, const float *norm_w, float eps,
                           uint32_t tokens, uint32_t h, uint16_t *y, float *xn) {
-    prof_begin(p, s, "to_bf16");
-    hipLaunchKernelGGL(to_bf16_kernel, dim3(tokens), dim3(64), 0, s, x, norm_w, eps, h, y, xn);
-    hipError_t e = hipGetLastError();
-    prof_end(p, s);
-    return e;
+    return launch_kernel(p, "to_bf16", to_bf16_kernel, dim3(tokens), dim3(64), 0, s, x, norm_w, eps,
+                         h, y, xn);
 }
 
 hipError_t launch_mfma_router(Prof *p, hipStream_t s, const WDesc &r, const uint16_t *xb16,
@@ -370,10 +368,7 @@ hipError_t launch_mfma_router(Prof *p, hipStream_t s, const WDesc &r, const uint
     a.out_f32 = logits;
     a.m_total = tokens;
     dim3 grid((tokens + kBM - 1) / kBM, (r.out + kBN - 1) / kBN);
-    prof_begin(p, s, "mfma_router");
-    hipError_t e = dispatch_kind(r, MfmaLaunch<MODE_ROUTER>{s, a, grid});
-    prof_end(p, s);
-    return e;
+    return dispatch_kind(r, MfmaLaunch<MODE_ROUTER>{p, "mfma_router", s, a, grid});
 }
 
 hipError_t launch_mfma_experts(Prof *p, hipStream_t s, const WDesc &gate, const WDesc &up,
@@ -382,11 +377,8 @@ hipError_t launch_mfma_experts(Prof *p, hipStream_t s, const WDesc &gate, const 
                                uint32_t pairs, uint32_t *tiles, uint32_t *ntiles,
                                uint16_t *act16, uint16_t *y16) {
     const uint32_t E = gate.experts;
-    prof_begin(p, s, "tile_schedule");
-    hipLaunchKernelGGL(tile_schedule_kernel, dim3(1), dim3(64), 0, s, offsets, E, gemm_tile_rows(),
-                       tiles, ntiles);
-    hipError_t e = hipGetLastError();
-    prof_end(p, s);
+    hipError_t e = launch_kernel(p, "tile_schedule", tile_schedule_kernel, dim3(1), dim3(64), 0, s,
+                                 offsets, E, gemm_tile_rows(), tiles, ntiles);
     if (e != hipSuccess) return e;
     e = launch_grouped_gemm(p, s, 0, gate, up, xb16, perm, offsets, tiles, ntiles, nullptr, k, act16);
     if (e != hipSuccess) return e;
@@ -396,13 +388,9 @@ hipError_t launch_mfma_experts(Prof *p, hipStream_t s, const WDesc &gate, const 
 hipError_t launch_combine16(Prof *p, hipStream_t s, const uint16_t *y16, const uint32_t *pos,
                             const float *wts, uint32_t k, const float *sh_out, const float *sh_gate,
                             const float *resid, float *out, uint32_t tokens, uint32_t h) {
-    prof_begin(p, s, "combine16");
     dim3 grid((h / 2 + 255) / 256, tokens);
-    hipLaunchKernelGGL(combine16_kernel, grid, dim3(256), 0, s, y16, pos, wts, k, sh_out, sh_gate,
-                       resid, out, h);
-    hipError_t e = hipGetLastError();
-    prof_end(p, s);
-    return e;
+    return launch_kernel(p, "combine16", combine16_kernel, grid, dim3(256), 0, s, y16, pos, wts, k,
+                         sh_out, sh_gate, resid, out, h);
 }
 
 }  // namespace moehip

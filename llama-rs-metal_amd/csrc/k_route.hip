@@ -18,12 +18,10 @@ __global__ __launch_bounds__(64) void route_kernel(const float *__restrict__ log
 
 hipError_t launch_route(Prof *p, hipStream_t s, const float *logits, uint32_t experts, uint32_t k,
                         int normalize, uint32_t tokens, uint32_t *ids, float *weights) {
-    prof_begin(p, s, "route");
-    hipLaunchKernelGGL(route_kernel, dim3(tokens), dim3(64), experts * sizeof(float), s, logits,
-                       experts, k, normalize, ids, weights);
-    hipError_t e = hipGetLastError();
-    prof_end(p, s);
-    return e;
+    // LDS copy of the logits only where the selection keeps one (route_one_wave)
+    const size_t lds = (experts > 1024 || k > 64) ? experts * sizeof(float) : 0;
+    return launch_kernel(p, "route", route_kernel, dim3(tokens), dim3(64), lds, s, logits, experts,
+                         k, normalize, ids, weights);
 }
 
 // ---------------------------------------------------------------- dispatch --
@@ -124,19 +122,19 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_place_kernel(
 hipError_t launch_dispatch(Prof *p, hipStream_t s, const uint32_t *ids, uint32_t pairs,
                            uint32_t experts, uint32_t *counts, uint32_t *offsets, uint32_t *perm,
                            uint32_t *pos) {
-    prof_begin(p, s, "dispatch");
     const uint32_t zb = (experts + kDispThreads - 1) / kDispThreads;
-    hipLaunchKernelGGL(zero_u32_kernel, dim3(zb), dim3(kDispThreads), 0, s, counts, experts);
+    hipError_t e = launch_kernel(p, "dispatch_zero", zero_u32_kernel, dim3(zb), dim3(kDispThreads), 0,
+                                 s, counts, experts);
+    if (e != hipSuccess) return e;
     const uint32_t per_block = kDispThreads * kDispItems;
     const uint32_t nb = (pairs + per_block - 1) / per_block;
-    if (nb)
-        hipLaunchKernelGGL(dispatch_count_kernel, dim3(nb), dim3(kDispThreads),
-                           experts * sizeof(uint32_t), s, ids, pairs, experts, counts);
-    hipLaunchKernelGGL(dispatch_place_kernel, dim3(experts), dim3(kDispThreads), 0, s, ids, pairs,
-                       experts, counts, offsets, perm, pos);
-    hipError_t e = hipGetLastError();
-    prof_end(p, s);
-    return e;
+    if (nb) {
+        e = launch_kernel(p, "dispatch_count", dispatch_count_kernel, dim3(nb), dim3(kDispThreads),
+                          experts * sizeof(uint32_t), s, ids, pairs, experts, counts);
+        if (e != hipSuccess) return e;
+    }
+    return launch_kernel(p, "dispatch_place", dispatch_place_kernel, dim3(experts),
+                         dim3(kDispThreads), 0, s, ids, pairs, experts, counts, offsets, perm, pos);
 }
 
 }  // namespace moehip

@@ -19,23 +19,20 @@ static hipEvent_t prof_event(Prof *p) {
     return e;
 }
 
-void prof_begin(Prof *p, hipStream_t s, const char *name) {
-    if (!p || !p->enabled || p->open >= 0) return;
+ProfEvents prof_launch(Prof *p, const char *name) {
+    if (!p || !p->enabled) return ProfEvents{nullptr, nullptr};
     size_t idx = p->entries.size();
     for (size_t i = 0; i < p->entries.size(); i++)
         if (p->entries[i].name == name) idx = i;
     if (idx == p->entries.size()) p->entries.push_back(ProfEntry{name, 0, 0.0});
     hipEvent_t a = prof_event(p), b = prof_event(p);
-    if (!a || !b) return;
-    (void)hipEventRecord(a, s);
+    if (!a || !b) {
+        if (a) p->pool.push_back(a);
+        if (b) p->pool.push_back(b);
+        return ProfEvents{nullptr, nullptr};
+    }
     p->pending.push_back(Prof::Pending{idx, a, b});
-    p->open = (int)p->pending.size() - 1;
-}
-
-void prof_end(Prof *p, hipStream_t s) {
-    if (!p || !p->enabled || p->open < 0) return;
-    (void)hipEventRecord(p->pending[p->open].b, s);
-    p->open = -1;
+    return ProfEvents{a, b};
 }
 
 void prof_collect(Prof *p, hipStream_t s) {

@@ -397,6 +397,14 @@ moe_status moe_profile_reset(moe_gpu *g) {
     return MOE_OK;
 }
 
+moe_status moe_profile_hold(moe_gpu *g, uint32_t microseconds) {
+    moe_status st = need_batch(g);
+    if (st) return st;
+    if (g->capturing) return shape(g, "hold inside a graph capture");
+    if (microseconds > 100000u) return shape(g, "hold longer than 100 ms");
+    return launched(g, launch_hold(g->stream, microseconds), "hold");
+}
+
 // ================================================================ graphs ==
 moe_status moe_graph_begin(moe_gpu *g) {
     moe_status st = need_no_batch(g);

@@ -1,7 +1,9 @@
 // Internal interfaces between the C ABI (moe_abi.cpp) and the kernel files.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
+#include <tuple>
 
 namespace moehip {
 
@@ -20,11 +22,35 @@ struct WDesc {
     uint32_t gshift;  // log2(group_size); 0 for dense
 };
 
-// Launch-side profiling hook: every launcher brackets its kernel with
-// prof_begin/prof_end (no-ops unless profiling is enabled on the gpu).
+// Launch-side profiling hook.  While profiling is enabled on the gpu,
+// prof_launch hands out a start/stop event pair that launch_kernel passes to
+// hipExtLaunchKernel: the events then carry the dispatch's own begin and end
+// timestamps (the kernel's execution, as a kernel trace reports it, without
+// the packet-processing time of separately recorded events).  Null events
+// when profiling is off.
 struct Prof;
-void prof_begin(Prof *p, hipStream_t s, const char *name);
-void prof_end(Prof *p, hipStream_t s);
+struct ProfEvents {
+    hipEvent_t start, stop;
+};
+ProfEvents prof_launch(Prof *p, const char *name);
+
+// kernel<<<grid, block, lds, s>>>(args...), timed under `name` when profiling.
+template <typename... KArgs, typename... Args>
+hipError_t launch_kernel(Prof *p, const char *name, void (*kernel)(KArgs...), dim3 grid,
+                         dim3 block, size_t lds, hipStream_t s, Args... args) {
+    static_assert(sizeof...(KArgs) == sizeof...(Args), "kernel argument count");
+    std::tuple<KArgs...> vals{static_cast<KArgs>(args)...};
+    void *ptrs[sizeof...(KArgs) > 0 ? sizeof...(KArgs) : 1];
+    std::apply([&ptrs](auto &...v) {
+        size_t i = 0;
+        ((ptrs[i++] = static_cast<void *>(&v)), ...);
+    }, vals);
+    const ProfEvents ev = prof_launch(p, name);
+    if (ev.start)
+        return hipExtLaunchKernel(reinterpret_cast<const void *>(kernel), grid, block, ptrs, lds, s,
+                                  ev.start, ev.stop, 0);
+    return hipLaunchKernel(reinterpret_cast<const void *>(kernel), grid, block, ptrs, lds, s);
+}
 
 // Work buffers of the fused/grouped MoE block (all device pointers).
 struct BlockBufs {
@@ -55,6 +81,7 @@ hipError_t launch_gemv(Prof *p, hipStream_t s, const WDesc &w, const float *x,
                        uint32_t tokens);
 
 // ---- routing + dispatch (k_route.hip) ----
+hipError_t launch_hold(hipStream_t s, uint32_t microseconds);
 hipError_t launch_route(Prof *p, hipStream_t s, const float *logits, uint32_t experts, uint32_t k,
                         int normalize, uint32_t tokens, uint32_t *ids, float *weights);
 hipError_t launch_dispatch(Prof *p, hipStream_t s, const uint32_t *ids, uint32_t pairs,

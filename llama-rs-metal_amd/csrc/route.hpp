@@ -85,16 +85,16 @@ __device__ __forceinline__ void route_wave_regs(const float *__restrict__ logits
 
 // LDS scratch of one routing wave.
 struct RouteLds {
-    alignas(16) uint64_t mk[64];  // composite keys of the 64 lanes' local bests
     alignas(16) uint64_t ck[64];  // composite keys of the surviving candidates
     uint32_t sj[64];  // selected ids by rank
     float sv[64];     // selected logits by rank
 };
 
-// Composite selection key: larger = earlier in the reference's scan order
-// (logit descending, index ascending); E < 65536.
-__device__ __forceinline__ uint64_t ckey(float v, uint32_t j) {
-    return ((uint64_t)fkey(v) << 16) | (uint64_t)(0xffffu - j);
+// Composite selection key of element j with value key k = fkey(v): larger =
+// earlier in the reference's scan order (logit descending, index ascending);
+// E < 65536.
+__device__ __forceinline__ uint64_t ckey(uint32_t k, uint32_t j) {
+    return ((uint64_t)k << 16) | (uint64_t)(0xffffu - j);
 }
 __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
@@ -106,78 +106,106 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_wave_barrier();
 }
 
-// Same selection as route_wave_regs without K serial passes (K <= 64):
-//  1. every lane finds its local best (strict `>` over ascending j);
-//  2. t = the K-th best of the 64 lane bests under the composite order: at
-//     least K elements are >= t, so every top-K element has logit >= t;
-//  3. the elements with logit >= t (NaN and -inf excluded) are compacted,
-//     and each is ranked against the others under the composite order.
-// Returns false (nothing written) when more than 64 candidates survive; the
-// caller then runs route_wave_regs.
+// Lane `lane` holds elements j = R*lane + i (i < R): two 16-byte loads per
+// lane when R is a multiple of 4 and the row is aligned and whole.
+template <int R>
+__device__ __forceinline__ void load_logits(const float *__restrict__ logits, uint32_t E, int lane,
+                                            float *v) {
+    const uint32_t j0 = (uint32_t)R * lane;
+    if constexpr (R % 4 == 0) {
+        if ((reinterpret_cast<uintptr_t>(logits) & 15u) == 0 && (uint64_t)R * kWave <= E) {
+#pragma unroll
+            for (int q = 0; q < R / 4; q++) {
+                const float4 f = reinterpret_cast<const float4 *>(logits + j0)[q];
+                v[4 * q + 0] = f.x;
+                v[4 * q + 1] = f.y;
+                v[4 * q + 2] = f.z;
+                v[4 * q + 3] = f.w;
+            }
+            return;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < R; i++) v[i] = j0 + i < E ? logits[j0 + i] : -INFINITY;
+}
+
+// Candidate ranking shared by the two selections below (K <= 64):
+//  1. key_i = fkey(v_i) for v_i > -inf (0 for -inf, NaN and padding, which
+//     never win the reference's strict `>` scan); kb = the lane's best key;
+//  2. t = the largest 16-bit key prefix that at least K lane bests reach
+//     (binary search over ballots): at least K elements have key >= t, so
+//     every top-K element does;
+//  3. the elements with key >= max(t, 1) are compacted into LDS and each is
+//     ranked against the others under the composite order (key descending,
+//     index ascending).
+// Returns the candidate count `total` (> 64: nothing ranked; the caller runs
+// route_wave_regs), and for lane < total its composite key `mine` and rank `r`.
+template <int R>
+__device__ __forceinline__ uint32_t rank_candidates(RouteLds *L, const float *v, uint32_t K,
+                                                    int lane, uint64_t &mine, uint32_t &r) {
+    uint32_t key[R], kb = 0;
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        key[i] = v[i] > -INFINITY ? fkey(v[i]) : 0u;
+        kb = max(kb, key[i]);
+    }
+    uint32_t t = 0;
+#pragma unroll
+    for (int b = 31; b >= 16; b--) {
+        const uint32_t c = t | (1u << b);
+        if ((uint32_t)__popcll(__ballot(kb >= c)) >= K) t = c;
+    }
+    const uint32_t tq = t ? t : 1u;
+    uint32_t total = 0, pos[R];
+    bool q[R];
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        q[i] = key[i] >= tq;
+        const uint64_t bm = __ballot(q[i]);
+        pos[i] = total + lanes_below(bm);
+        total += (uint32_t)__popcll(bm);
+    }
+    if (total > (uint32_t)kWave) return total;
+#pragma unroll
+    for (int i = 0; i < R; i++)
+        if (q[i]) L->ck[pos[i]] = ckey(key[i], (uint32_t)R * lane + i);
+    if (total & 1u) L->ck[total] = 0ull;  // pad to whole pairs (odd total < 64); 0 ranks last
+    wave_lds_sync();
+    mine = (uint32_t)lane < total ? L->ck[lane] : 0ull;
+    r = 0;
+    for (uint32_t c = 0; c < total; c += 2) {
+        const ulonglong2 p = *reinterpret_cast<const ulonglong2 *>(&L->ck[c]);
+        r += (p.x > mine ? 1u : 0u) + (p.y > mine ? 1u : 0u);
+    }
+    return total;
+}
+
+// Full selection (ids and weights) without K serial passes.  Returns false
+// (nothing written) when more than 64 candidates survive; the caller then
+// runs route_wave_regs.
 template <int R>
 __device__ __forceinline__ bool route_wave_rank(RouteLds *L, const float *__restrict__ logits,
                                                 uint32_t E, uint32_t K, int normalize,
                                                 uint32_t *ids, float *weights, int lane) {
     float v[R];
-#pragma unroll
-    for (int i = 0; i < R; i++) {
-        const uint32_t j = lane + kWave * i;
-        v[i] = j < E ? logits[j] : -INFINITY;
-    }
-    float lm = -INFINITY, m = -INFINITY;
-    int li = R;
-#pragma unroll
-    for (int i = 0; i < R; i++) {
-        if (v[i] > lm) {
-            lm = v[i];
-            li = i;
-        }
-        m = fmaxf(m, v[i]);
-    }
-    const uint64_t my = li < R ? ckey(lm, lane + kWave * li) : 0ull;
-    L->mk[lane] = my;
-    const float mx = wave_max(m);
-    float den = 0.f;
-#pragma unroll
-    for (int i = 0; i < R; i++)
-        if (lane + kWave * i < E) den += exp_fast(v[i] - mx);
-    wave_lds_sync();
-    uint32_t rank = 0;
-#pragma unroll
-    for (int c = 0; c < kWave; c += 2) {
-        const ulonglong2 q = *reinterpret_cast<const ulonglong2 *>(&L->mk[c]);
-        rank += (q.x > my ? 1u : 0u) + (q.y > my ? 1u : 0u);
-    }
-    den = wave_sum(den);
-    const uint64_t tm = __ballot(rank == K - 1);
-    uint32_t tval = 0;  // no lane at rank K-1: fewer than K lane bests -> keep all
-    if (tm) tval = (uint32_t)(readlane_u((uint32_t)(my >> 32), __ffsll((unsigned long long)tm) - 1) << 16 |
-                              readlane_u((uint32_t)my, __ffsll((unsigned long long)tm) - 1) >> 16);
-    uint32_t total = 0, pos[R];
-    bool q[R];
-#pragma unroll
-    for (int i = 0; i < R; i++) {
-        q[i] = v[i] > -INFINITY && fkey(v[i]) >= tval;
-        const uint64_t bm = __ballot(q[i]);
-        pos[i] = total + lanes_below(bm);
-        total += (uint32_t)__popcll(bm);
-    }
+    load_logits<R>(logits, E, lane, v);
+    uint64_t mine;
+    uint32_t r;
+    const uint32_t total = rank_candidates<R>(L, v, K, lane, mine, r);
     if (total > (uint32_t)kWave) return false;
-#pragma unroll
-    for (int i = 0; i < R; i++)
-        if (q[i]) L->ck[pos[i]] = ckey(v[i], lane + kWave * i);
-    if (total & 1u) L->ck[total] = 0ull;  // pad to whole pairs (odd total < 64); 0 ranks last
-    wave_lds_sync();
-    const uint64_t mine = (uint32_t)lane < total ? L->ck[lane] : 0ull;
-    uint32_t r = 0;
-    for (uint32_t c = 0; c < total; c += 2) {
-        const ulonglong2 q = *reinterpret_cast<const ulonglong2 *>(&L->ck[c]);
-        r += (q.x > mine ? 1u : 0u) + (q.y > mine ? 1u : 0u);
-    }
     if ((uint32_t)lane < total && r < K) {
         L->sj[r] = 0xffffu - (uint32_t)(mine & 0xffffu);
         L->sv[r] = funkey((uint32_t)(mine >> 16));
     }
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < R; i++) m = fmaxf(m, v[i]);
+    const float mx = wave_max(m);
+    float den = 0.f;
+#pragma unroll
+    for (int i = 0; i < R; i++)
+        if ((uint32_t)R * lane + i < E) den += exp_fast(v[i] - mx);
+    den = wave_sum(den);
     wave_lds_sync();
     float score = -INFINITY;  // ranks beyond the candidates: id 0, score -inf
     uint32_t id = 0;
@@ -265,6 +293,40 @@ __device__ __forceinline__ void route_one_wave(RouteLds *L, float *vals,
         route_regs<8>(L, logits, E, K, normalize, ids, weights, lane);
     else
         route_regs<16>(L, logits, E, K, normalize, ids, weights, lane);
+}
+
+// Only the id selected by pass `want` (want < K <= 64) of the same routing;
+// no weights.  Every lane returns it.
+template <int R>
+__device__ __forceinline__ uint32_t route_id_regs(RouteLds *L, const float *__restrict__ logits,
+                                                  uint32_t E, uint32_t K, uint32_t want, int lane) {
+    float v[R];
+    load_logits<R>(logits, E, lane, v);
+    uint64_t mine;
+    uint32_t r;
+    const uint32_t total = rank_candidates<R>(L, v, K, lane, mine, r);
+    if (total <= (uint32_t)kWave) {
+        const uint64_t hit = __ballot((uint32_t)lane < total && r == want);
+        if (!hit) return 0u;  // exhausted pool: id 0
+        return readlane_u(0xffffu - (uint32_t)(mine & 0xffffu), __ffsll((unsigned long long)hit) - 1);
+    }
+    route_wave_regs<R>(logits, E, K, 0, L->sj, L->sv, lane);
+    wave_lds_sync();
+    return L->sj[want];
+}
+__device__ __forceinline__ uint32_t route_one_id(RouteLds *L, float *vals,
+                                                 const float *__restrict__ logits, uint32_t E,
+                                                 uint32_t K, uint32_t want, int lane) {
+    if (E > 1024) {
+        route_wave_lds(vals, logits, E, K, 0, L->sj, L->sv, lane);
+        wave_lds_sync();
+        return L->sj[want];
+    }
+    if (E <= 64) return route_id_regs<1>(L, logits, E, K, want, lane);
+    if (E <= 128) return route_id_regs<2>(L, logits, E, K, want, lane);
+    if (E <= 256) return route_id_regs<4>(L, logits, E, K, want, lane);
+    if (E <= 512) return route_id_regs<8>(L, logits, E, K, want, lane);
+    return route_id_regs<16>(L, logits, E, K, want, lane);
 }
 
 }  // namespace moehip

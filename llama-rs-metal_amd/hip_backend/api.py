@@ -144,6 +144,7 @@ SIGNATURES = {
     "moe_profile_get": (I32, [P, U32, C.c_char_p, C.c_size_t, C.POINTER(U64),
                               C.POINTER(C.c_double)]),
     "moe_profile_reset": (I32, [P]),
+    "moe_profile_hold": (I32, [P, U32]),
     "moe_graph_begin": (I32, [P]),
     "moe_graph_end": (I32, [P, C.POINTER(C.c_void_p)]),
     "moe_graph_launch": (I32, [P, P]),
@@ -552,3 +553,9 @@ class Batch:
 
     def graph(self, graph):
         self._ck(_lib.moe_graph_launch(self.gpu._h, graph.h))
+
+    def hold(self, microseconds):
+        """Occupy the stream for `microseconds` so the launches enqueued next
+        are queued before the GPU reaches them (profiled durations then
+        exclude host enqueue gaps)."""
+        self._ck(_lib.moe_profile_hold(self.gpu._h, int(microseconds)))

@@ -12,7 +12,7 @@ import pytest
 import oracle
 from helpers import (close, config1, config2, config3, config4, config5, hot_bias, rel_max_err,
                      zipf_bias)
-from hip_backend import PATH_AUTO, PATH_GROUPED, PATH_MFMA, PATH_OPS, synth
+from hip_backend import PATH_AUTO, PATH_GROUPED, PATH_MFMA, PATH_OPS, BlockWeights, Tensor, synth
 
 pytestmark = pytest.mark.gpu
 
@@ -96,6 +96,31 @@ def test_config2_decode_fused(gpu, c2):
         x = synth.normal(1000 + seed, 2048).reshape(1, 2048)
         print(f"[case] config2 fused seed={seed}", flush=True)
         check_against_oracle(blk, x, run_block(gpu, bw, x, 1, PATH_AUTO))
+
+
+@pytest.mark.parametrize("levels", [5, 64])
+def test_config2_decode_tied_logits(gpu, c2, levels):
+    """Zero router plus a bias drawn from `levels` values: the logits are the
+    bias exactly, full of ties.  Each gate/up wave selects its expert on its
+    own, so the output only matches the oracle if every selection breaks the
+    ties toward the lower index (5 levels: ~100 experts share the top value,
+    more candidates than one wave ranks; 64 levels: ~8 per value)."""
+    import copy
+    blk, bw = c2
+    zero = Tensor.dense([2048, 512], np.zeros(2048 * 512, np.float32))
+    blk0 = copy.copy(blk)
+    blk0.router = zero
+    _, gate, up, down, shared, sgi = bw.keep
+    bw0 = BlockWeights(gpu.weight_tensor(zero), gate, up, down, bw.k, True, shared, sgi)
+    rng = np.random.default_rng(49 + levels)
+    vals = np.linspace(-2.0, 2.0, levels).astype(np.float32)
+    for seed in range(2):
+        bias = vals[rng.integers(0, levels, 512)].reshape(1, 512)
+        x = synth.normal(1500 + seed, 2048).reshape(1, 2048)
+        print(f"[case] config2 tied logits levels={levels} seed={seed}", flush=True)
+        got = run_block(gpu, bw0, x, 1, PATH_AUTO, bias=bias)
+        assert np.array_equal(got[1], bias)
+        check_against_oracle(blk0, x, got, bias=bias)
 
 
 def test_config2_paths_agree(gpu, c2):
