@@ -29,6 +29,25 @@ __device__ __forceinline__ float load_scalar(const void *p, uint64_t i) {
     }
 }
 
+// Raw bits of one such scalar, converted later by raw_to_f32: lets a caller
+// issue every load before the first conversion waits on one.
+template <int T>
+__device__ __forceinline__ uint32_t load_raw(const void *p, uint64_t i) {
+    if constexpr (T == 0)
+        return reinterpret_cast<const uint32_t *>(p)[i];
+    else
+        return reinterpret_cast<const uint16_t *>(p)[i];
+}
+template <int T>
+__device__ __forceinline__ float raw_to_f32(uint32_t r) {
+    if constexpr (T == 0)
+        return __uint_as_float(r);
+    else if constexpr (T == 30)
+        return bf16_to_f32(r);
+    else
+        return f16_to_f32(r);
+}
+
 // ---- cross-lane reductions: DPP within 16-lane rows, gfx950 permlane swaps
 // across rows (no LDS round trips, no SGPR round trips).  All lanes of the
 // wave must be active.  dpp_ctrl codes (gfx9 DPP): quad_perm [1,0,3,2],

@@ -67,37 +67,55 @@ struct Chunk32 {
     }
 };
 
-// One lane's share of `R` rows: chunk loads (and group scale/bias loads) are
-// all issued before any arithmetic so R rows are in flight per lane.
-// rows[f] >= nrows marks an absent row (contributes 0).
+// One lane's share of `R` rows, split into a load phase and an arithmetic
+// phase so a caller can put several row sets (and its activation loads) in
+// flight before the first wait.  Loads are unconditional: a load under a
+// branch, or a conversion next to its load, makes the compiler wait for it
+// before the next row's loads issue.  An absent row (!ok[f]) re-reads row 0
+// and contributes 0.
+template <int BITS, int T, int R>
+struct LaneRows {
+    Chunk32<BITS, T> c[R];
+    uint32_t sr[R], br[R];
+    bool ok[R];
+    __device__ __forceinline__ void load(const WDesc &w, const uint64_t *grow, const bool *okv,
+                                         uint32_t cl, uint32_t C) {
+#pragma unroll
+        for (int f = 0; f < R; f++) {
+            ok[f] = okv[f];
+            const uint64_t row = okv[f] ? grow[f] : 0u;
+            c[f].load(w.data, row * C + cl);
+            if constexpr (BITS) {
+                const uint64_t g = (row * w.in + (uint64_t)cl * 32) >> w.gshift;
+                sr[f] = load_raw<T>(w.scales, g);
+                br[f] = load_raw<T>(w.biases, g);
+            }
+        }
+    }
+    __device__ __forceinline__ void dot(const float *x, float xsum, float *res) const {
+#pragma unroll
+        for (int f = 0; f < R; f++) {
+            float v;
+            if constexpr (BITS)
+                v = raw_to_f32<T>(sr[f]) * c[f].dot(x) + raw_to_f32<T>(br[f]) * xsum;
+            else
+                v = c[f].dot(x);
+            res[f] = ok[f] ? v : 0.f;
+        }
+    }
+};
+
+// Issue point: every load above it issues before the arithmetic below it.
+__device__ __forceinline__ void loads_issued() { __builtin_amdgcn_sched_barrier(0); }
+
 template <int BITS, int T, int R>
 __device__ __forceinline__ void lane_rows_dot(const WDesc &w, const uint64_t *grow, const bool *ok,
                                               uint32_t cl, uint32_t C, const float *x, float xsum,
                                               float *res) {
-    Chunk32<BITS, T> c[R];
-    float s[R], b[R];
-#pragma unroll
-    for (int f = 0; f < R; f++) {
-        if (ok[f]) {
-            c[f].load(w.data, grow[f] * C + cl);
-            if constexpr (BITS) {
-                const uint64_t g = (grow[f] * w.in + (uint64_t)cl * 32) >> w.gshift;
-                s[f] = load_scalar<T>(w.scales, g);
-                b[f] = load_scalar<T>(w.biases, g);
-            }
-        }
-    }
-#pragma unroll
-    for (int f = 0; f < R; f++) {
-        float v = 0.f;
-        if (ok[f]) {
-            if constexpr (BITS)
-                v = s[f] * c[f].dot(x) + b[f] * xsum;
-            else
-                v = c[f].dot(x);
-        }
-        res[f] = v;
-    }
+    LaneRows<BITS, T, R> L;
+    L.load(w, grow, ok, cl, C);
+    loads_issued();
+    L.dot(x, xsum, res);
 }
 
 // Single row of any kind (wave-uniform switch on the weight's kind).
@@ -121,42 +139,54 @@ __device__ __forceinline__ float lane_row_dot_any(const WDesc &w, uint64_t grow,
     return r;
 }
 
-// This lane's 32-element slice of the (optionally RMS-normalised) input.
-// RMSNorm (crates/metal-backend/src/shaders/elementwise.metal:31-46): the sum
-// of squares is reduced over the `width` lanes that span the row.
-__device__ __forceinline__ float load_x_chunk(const float *__restrict__ x,
-                                              const float *__restrict__ norm_w, float eps,
-                                              uint32_t h, uint32_t cl, int width, float *xr) {
-    const float4 *src = reinterpret_cast<const float4 *>(x + (uint64_t)cl * 32);
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const float4 v = src[i];
-        xr[4 * i + 0] = v.x;
-        xr[4 * i + 1] = v.y;
-        xr[4 * i + 2] = v.z;
-        xr[4 * i + 3] = v.w;
-    }
-    if (norm_w) {
-        float ss = 0.f;
-#pragma unroll
-        for (int j = 0; j < 32; j++) ss += xr[j] * xr[j];
-        ss = subwave_sum(ss, width);
-        const float inv = 1.0f / sqrtf(ss / (float)h + eps);
-        const float4 *wv = reinterpret_cast<const float4 *>(norm_w + (uint64_t)cl * 32);
+// This lane's 32-element slice of the (optionally RMS-normalised) input,
+// loaded first (load) and normalised once the caller's other loads are in
+// flight (finish).  RMSNorm (crates/metal-backend/src/shaders/
+// elementwise.metal:31-46): the sum of squares is reduced over the `width`
+// lanes that span the row.
+struct XChunk {
+    float xr[32];
+    float nw[32];
+    __device__ __forceinline__ void load(const float *__restrict__ x,
+                                         const float *__restrict__ norm_w, uint32_t cl) {
+        const float4 *src = reinterpret_cast<const float4 *>(x + (uint64_t)cl * 32);
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const float4 v = wv[i];
-            xr[4 * i + 0] = xr[4 * i + 0] * inv * v.x;
-            xr[4 * i + 1] = xr[4 * i + 1] * inv * v.y;
-            xr[4 * i + 2] = xr[4 * i + 2] * inv * v.z;
-            xr[4 * i + 3] = xr[4 * i + 3] * inv * v.w;
+            const float4 v = src[i];
+            xr[4 * i + 0] = v.x;
+            xr[4 * i + 1] = v.y;
+            xr[4 * i + 2] = v.z;
+            xr[4 * i + 3] = v.w;
+        }
+        if (norm_w) {
+            const float4 *wv = reinterpret_cast<const float4 *>(norm_w + (uint64_t)cl * 32);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float4 v = wv[i];
+                nw[4 * i + 0] = v.x;
+                nw[4 * i + 1] = v.y;
+                nw[4 * i + 2] = v.z;
+                nw[4 * i + 3] = v.w;
+            }
         }
     }
-    float xsum = 0.f;
+    // Normalises in place (when norm_w) and returns the slice's sum.
+    __device__ __forceinline__ float finish(const float *norm_w, float eps, uint32_t h, int width) {
+        if (norm_w) {
+            float ss = 0.f;
 #pragma unroll
-    for (int j = 0; j < 32; j++) xsum += xr[j];
-    return xsum;
-}
+            for (int j = 0; j < 32; j++) ss += xr[j] * xr[j];
+            ss = subwave_sum(ss, width);
+            const float inv = 1.0f / sqrtf(ss / (float)h + eps);
+#pragma unroll
+            for (int j = 0; j < 32; j++) xr[j] = xr[j] * inv * nw[j];
+        }
+        float xsum = 0.f;
+#pragma unroll
+        for (int j = 0; j < 32; j++) xsum += xr[j];
+        return xsum;
+    }
+};
 
 struct DecodeKArgs {
     WDesc router, gate, up, down, sg, su, sd, sgi;
@@ -260,13 +290,17 @@ constexpr int kDownFR = 2;    // output rows per sub-wave in decode_down
 // One wave per block: router rows (and the shared expert's scalar gate row).
 template <int BR, int TR>
 __device__ __forceinline__ void router_item(const DecodeKArgs &a, uint32_t wave_id, uint32_t sub,
-                                            uint32_t cl, const float *xr, float xsum) {
+                                            uint32_t cl, XChunk &X) {
     // router GEMV rows (Batch::matmul(router), crates/model-runtime/src/execute.rs:220)
     const uint32_t lpr = a.lpr_h, rpi = 64u / lpr;
     const uint64_t e = (uint64_t)wave_id * rpi + sub;
     const bool ok = e < a.E;
+    LaneRows<BR, TR, 1> L;
+    L.load(a.router, &e, &ok, cl, a.h / 32);
+    loads_issued();
+    const float xsum = X.finish(a.norm_w, a.eps, a.h, (int)lpr);
     float v;
-    lane_rows_dot<BR, TR, 1>(a.router, &e, &ok, cl, a.h / 32, xr, xsum, &v);
+    L.dot(X.xr, xsum, &v);
     v = subwave_sum(v, (int)lpr);
     if (ok && cl == 0) a.logits[e] = a.logit_bias ? v + a.logit_bias[e] : v;
 }
@@ -276,29 +310,30 @@ __global__ __launch_bounds__(64) void decode_pre_kernel(DecodeKArgs a) {
     const int lane = threadIdx.x;
     const uint32_t wave_id = blockIdx.x;
     const uint32_t lpr = a.lpr_h, sub = lane / lpr, cl = lane % lpr;
-    float xr[32];
-    const float xsum = load_x_chunk(a.x, a.norm_w, a.eps, a.h, cl, (int)lpr, xr);
+    XChunk X;
+    X.load(a.x, a.norm_w, cl);
     if (wave_id < a.n_router_waves) {
         const WDesc &r = a.router;
         switch (r.bits) {
-        case 2: router_item<2, ST>(a, wave_id, sub, cl, xr, xsum); break;
-        case 4: router_item<4, ST>(a, wave_id, sub, cl, xr, xsum); break;
-        case 8: router_item<8, ST>(a, wave_id, sub, cl, xr, xsum); break;
+        case 2: router_item<2, ST>(a, wave_id, sub, cl, X); break;
+        case 4: router_item<4, ST>(a, wave_id, sub, cl, X); break;
+        case 8: router_item<8, ST>(a, wave_id, sub, cl, X); break;
         default:
             if (r.type == 0)
-                router_item<0, 0>(a, wave_id, sub, cl, xr, xsum);
+                router_item<0, 0>(a, wave_id, sub, cl, X);
             else if (r.type == 1)
-                router_item<0, 1>(a, wave_id, sub, cl, xr, xsum);
+                router_item<0, 1>(a, wave_id, sub, cl, X);
             else
-                router_item<0, 30>(a, wave_id, sub, cl, xr, xsum);
+                router_item<0, 30>(a, wave_id, sub, cl, X);
         }
         return;
     }
     if (a.has_shared && wave_id == a.n_router_waves) {
         // shared-expert gate input [h] -> scalar (matmul(shared_gate [h,1]),
         // execute.rs:230; weight reshaped [h] -> [h,1], loader.rs:194)
+        const float xsum = X.finish(a.norm_w, a.eps, a.h, (int)lpr);
         float v = 0.f;
-        if (sub == 0) v = lane_row_dot_any<ST>(a.sgi, 0, cl, a.h / 32, xr, xsum);
+        if (sub == 0) v = lane_row_dot_any<ST>(a.sgi, 0, cl, a.h / 32, X.xr, xsum);
         v = subwave_sum(v, (int)lpr);
         if (lane == 0) a.sh_gate[0] = v;
     }
@@ -307,7 +342,7 @@ __global__ __launch_bounds__(64) void decode_pre_kernel(DecodeKArgs a) {
 // --------------------------------------------------------------- gate/up --
 template <int BS, int ST>
 __device__ __forceinline__ void shared_item(const DecodeKArgs &a, uint32_t item, uint32_t sub,
-                                            uint32_t cl, const float *xr, float xsum) {
+                                            uint32_t cl, XChunk &X) {
     // shared expert gate/up + SwiGLU (encode_dense, execute.rs:258-264)
     const uint32_t lpr = a.lpr_h, rpi = 64u / lpr;
     uint64_t rows[kGateFR];
@@ -317,9 +352,14 @@ __device__ __forceinline__ void shared_item(const DecodeKArgs &a, uint32_t item,
         rows[f] = ((uint64_t)item * kGateFR + f) * rpi + sub;
         ok[f] = rows[f] < a.ffs;
     }
+    LaneRows<BS, ST, kGateFR> Lg, Lu;
+    Lg.load(a.sg, rows, ok, cl, a.h / 32);
+    Lu.load(a.su, rows, ok, cl, a.h / 32);
+    loads_issued();
+    const float xsum = X.finish(a.norm_w, a.eps, a.h, (int)lpr);
     float g[kGateFR], u[kGateFR];
-    lane_rows_dot<BS, ST, kGateFR>(a.sg, rows, ok, cl, a.h / 32, xr, xsum, g);
-    lane_rows_dot<BS, ST, kGateFR>(a.su, rows, ok, cl, a.h / 32, xr, xsum, u);
+    Lg.dot(X.xr, xsum, g);
+    Lu.dot(X.xr, xsum, u);
     gateup_epilogue(g, u, (int)(sub * lpr + cl), lpr, rpi, sub, cl, item, a.ffs, a.sh_act);
 }
 
@@ -337,15 +377,15 @@ __global__ __launch_bounds__(64) void decode_gateup_kernel(DecodeKArgs a) {
     const uint32_t lpr = a.lpr_h, rpi = 64u / lpr, sub = lane / lpr, cl = lane % lpr;
     const uint32_t wave_id = blockIdx.x;
     const uint32_t routed_waves = a.k * a.n_gate_waves_per_expert;
-    float xr[32];
-    const float xsum = load_x_chunk(a.x, a.norm_w, a.eps, a.h, cl, (int)lpr, xr);
+    XChunk X;
+    X.load(a.x, a.norm_w, cl);
     if (wave_id >= routed_waves) {
         if (!a.has_shared) return;
         const uint32_t item = wave_id - routed_waves;
         switch (a.sg.bits) {
-        case 2: shared_item<2, ST>(a, item, sub, cl, xr, xsum); break;
-        case 4: shared_item<4, ST>(a, item, sub, cl, xr, xsum); break;
-        default: shared_item<8, ST>(a, item, sub, cl, xr, xsum); break;
+        case 2: shared_item<2, ST>(a, item, sub, cl, X); break;
+        case 4: shared_item<4, ST>(a, item, sub, cl, X); break;
+        default: shared_item<8, ST>(a, item, sub, cl, X); break;
         }
         return;
     }
@@ -374,9 +414,14 @@ __global__ __launch_bounds__(64) void decode_gateup_kernel(DecodeKArgs a) {
         ok[f] = j < a.ff;
         rows[f] = (uint64_t)e * a.ff + j;
     }
+    LaneRows<BITS, ST, kGateFR> Lg, Lu;
+    Lg.load(a.gate, rows, ok, cl, a.h / 32);
+    Lu.load(a.up, rows, ok, cl, a.h / 32);
+    loads_issued();
+    const float xsum = X.finish(a.norm_w, a.eps, a.h, (int)lpr);
     float g[kGateFR], u[kGateFR];
-    lane_rows_dot<BITS, ST, kGateFR>(a.gate, rows, ok, cl, a.h / 32, xr, xsum, g);
-    lane_rows_dot<BITS, ST, kGateFR>(a.up, rows, ok, cl, a.h / 32, xr, xsum, u);
+    Lg.dot(X.xr, xsum, g);
+    Lu.dot(X.xr, xsum, u);
     gateup_epilogue(g, u, lane, lpr, rpi, sub, cl, item, a.ff, a.act + (uint64_t)kk * a.ff);
 }
 
@@ -387,23 +432,6 @@ __global__ __launch_bounds__(64) void decode_gateup_kernel(DecodeKArgs a) {
 // sums meet in LDS.
 constexpr int kDownMaxWaves = 16;
 constexpr int kDownMaxPerWave = 2;
-
-template <int BITS, int ST>
-__device__ __forceinline__ void load_act_chunk(const float *act_row, uint32_t cl, float *xr,
-                                               float &xsum) {
-    const float4 *src = reinterpret_cast<const float4 *>(act_row + (uint64_t)cl * 32);
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const float4 v = src[i];
-        xr[4 * i + 0] = v.x;
-        xr[4 * i + 1] = v.y;
-        xr[4 * i + 2] = v.z;
-        xr[4 * i + 3] = v.w;
-    }
-    xsum = 0.f;
-#pragma unroll
-    for (int j = 0; j < 32; j++) xsum += xr[j];
-}
 
 template <int BITS, int ST, int BS>
 __device__ __forceinline__ void down_wave(const DecodeKArgs &a, uint32_t wv, uint32_t nw,
@@ -417,29 +445,36 @@ __device__ __forceinline__ void down_wave(const DecodeKArgs &a, uint32_t wv, uin
         if (kk >= n_exp) break;
         uint64_t rows[kDownFR];
         bool ok[kDownFR];
-        float xr[32], xsum, part[kDownFR];
+        float part[kDownFR];
+        XChunk X;  // this expert's SwiGLU activations (no norm)
         if (kk < a.k) {
             const uint32_t e = a.ids[kk];
+            const float wk = a.weights[kk];
+            X.load(a.act + (uint64_t)kk * a.ff, nullptr, cl);
 #pragma unroll
             for (int f = 0; f < kDownFR; f++) {
                 const uint32_t r = row0 + f * rpi + sub;
                 ok[f] = r < a.h;
                 rows[f] = (uint64_t)e * a.h + r;
             }
-            load_act_chunk<BITS, ST>(a.act + (uint64_t)kk * a.ff, cl, xr, xsum);
-            lane_rows_dot<BITS, ST, kDownFR>(a.down, rows, ok, cl, C, xr, xsum, part);
-            const float wk = a.weights[kk];
+            LaneRows<BITS, ST, kDownFR> L;
+            L.load(a.down, rows, ok, cl, C);
+            loads_issued();
+            L.dot(X.xr, X.finish(nullptr, 0.f, 0, 0), part);
 #pragma unroll
             for (int f = 0; f < kDownFR; f++) acc_r[f] += part[f] * wk;
         } else {
+            X.load(a.sh_act, nullptr, cl);
 #pragma unroll
             for (int f = 0; f < kDownFR; f++) {
                 const uint32_t r = row0 + f * rpi + sub;
                 ok[f] = r < a.h;
                 rows[f] = r;
             }
-            load_act_chunk<BITS, ST>(a.sh_act, cl, xr, xsum);
-            lane_rows_dot<BS, ST, kDownFR>(a.sd, rows, ok, cl, C, xr, xsum, part);
+            LaneRows<BS, ST, kDownFR> L;
+            L.load(a.sd, rows, ok, cl, C);
+            loads_issued();
+            L.dot(X.xr, X.finish(nullptr, 0.f, 0, 0), part);
 #pragma unroll
             for (int f = 0; f < kDownFR; f++) acc_s[f] += part[f];
         }
