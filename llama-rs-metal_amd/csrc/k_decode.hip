@@ -1,10 +1,11 @@
 // Fused single-token MoE decode: three launches per layer.
 //
-//   decode_pre     router GEMV (+logit bias) and, independent of routing, the
-//                  shared expert's gate/up/SwiGLU and its scalar gate input.
-//   decode_gateup  every block re-derives the top-k routing from the logits
-//                  (one wave, exact), then streams the selected experts'
-//                  gate/up rows and writes SwiGLU activations.
+//   decode_pre     router GEMV (+logit bias) and the shared expert's scalar
+//                  gate input.
+//   decode_gateup  every one-wave block re-derives its selection pass of the
+//                  top-k routing from the logits (exact), then streams that
+//                  expert's gate/up rows; blocks of the shared expert (no
+//                  routing) stream theirs; all write SwiGLU activations.
 //   decode_down    down rows of the K routed experts and the shared expert,
 //                  weighted combine, sigmoid shared gate and residual.
 //
