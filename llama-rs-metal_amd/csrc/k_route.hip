@@ -24,6 +24,38 @@ hipError_t launch_route(Prof *p, hipStream_t s, const float *logits, uint32_t ex
                          k, normalize, ids, weights);
 }
 
+// Routing of router products split over K: logits[t, j] = sum_s part[s, t, j]
+// (s ascending) + bias[t, j], written out and routed by the token's wave.
+__global__ __launch_bounds__(64) void route_sum_kernel(const float *__restrict__ parts,
+                                                       uint32_t nsplit, const float *__restrict__ bias,
+                                                       uint32_t E, uint32_t K, int normalize,
+                                                       float *__restrict__ logits,
+                                                       uint32_t *__restrict__ ids,
+                                                       float *__restrict__ weights) {
+    extern __shared__ __attribute__((aligned(16))) float lg[];  // E logits of this token
+    __shared__ RouteLds L;
+    const uint32_t t = blockIdx.x;
+    const uint64_t row = (uint64_t)t * E, stride = (uint64_t)gridDim.x * E;
+    for (uint32_t j = threadIdx.x; j < E; j += kWave) {
+        float v = parts[row + j];
+        for (uint32_t s = 1; s < nsplit; s++) v += parts[s * stride + row + j];
+        if (bias) v += bias[row + j];
+        logits[row + j] = v;
+        lg[j] = v;
+    }
+    wave_lds_sync();
+    route_one_wave(&L, lg, lg, E, K, normalize, ids + (uint64_t)t * K, weights + (uint64_t)t * K,
+                   threadIdx.x);
+}
+
+hipError_t launch_route_sum(Prof *p, hipStream_t s, const float *parts, uint32_t nsplit,
+                            const float *bias, uint32_t experts, uint32_t k, int normalize,
+                            uint32_t tokens, float *logits, uint32_t *ids, float *weights) {
+    return launch_kernel(p, "route", route_sum_kernel, dim3(tokens), dim3(64),
+                         experts * sizeof(float), s, parts, nsplit, bias, experts, k, normalize,
+                         logits, ids, weights);
+}
+
 // ---------------------------------------------------------------- dispatch --
 // Pass 1: per-expert counts.  LDS histogram per block, then one global
 // atomic per touched expert; the totals are independent of atomic order.

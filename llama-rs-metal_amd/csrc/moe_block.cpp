@@ -215,13 +215,28 @@ moe_status run_mfma(moe_gpu *g, const moe_block_weights *w, const Dims &d, const
     const float *xin = nw ? xn : xraw;  // F32 input of the VALU products
     const WDesc R = wdesc(w->router);
     const float *bias = has(io->logit_bias) ? fp(io->logit_bias) : nullptr;
-    if (mfma_supported(R)) {
-        TRY(launch_mfma_router(p, s, R, xb16, (uint32_t)T, bias, logits));
+    if (gemm_supported(R)) {
+        // partial sums of the K ranges staged in y16, free until the down GEMM
+        float *parts = reinterpret_cast<float *>(y16);
+        const uint64_t part_floats = (uint64_t)T * K * d.h / 2;
+        const uint32_t ks = gemm_router_ksplit(R, (uint32_t)T, part_floats);
+        if (ks > 1) {
+            TRY(launch_gemm_router(p, s, R, xb16, (uint32_t)T, ks, nullptr, parts));
+            TRY(launch_route_sum(p, s, parts, ks, bias, E, K, w->normalize ? 1 : 0, (uint32_t)T,
+                                 logits, ids, wts));
+        } else {
+            TRY(launch_gemm_router(p, s, R, xb16, (uint32_t)T, 1, bias, logits));
+            TRY(launch_route(p, s, logits, E, K, w->normalize ? 1 : 0, (uint32_t)T, ids, wts));
+        }
     } else {
-        TRY(launch_gemv(p, s, R, xin, 0, nullptr, 1, logits, (uint32_t)T));
-        if (bias) TRY(launch_add(p, s, logits, bias, logits, T * d.E));
+        if (mfma_supported(R)) {
+            TRY(launch_mfma_router(p, s, R, xb16, (uint32_t)T, bias, logits));
+        } else {
+            TRY(launch_gemv(p, s, R, xin, 0, nullptr, 1, logits, (uint32_t)T));
+            if (bias) TRY(launch_add(p, s, logits, bias, logits, T * d.E));
+        }
+        TRY(launch_route(p, s, logits, E, K, w->normalize ? 1 : 0, (uint32_t)T, ids, wts));
     }
-    TRY(launch_route(p, s, logits, E, K, w->normalize ? 1 : 0, (uint32_t)T, ids, wts));
     TRY(launch_dispatch(p, s, ids, (uint32_t)(T * K), E, counts, offsets, perm, pos));
     TRY(launch_mfma_experts(p, s, wdesc(w->gate), wdesc(w->up), wdesc(w->down), xb16, offsets, perm,
                             wts, K, (uint32_t)(T * K), tiles, ntiles, act16, y16));

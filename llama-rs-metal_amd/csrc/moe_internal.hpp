@@ -82,6 +82,16 @@ hipError_t launch_gemv(Prof *p, hipStream_t s, const WDesc &w, const float *x,
 
 // ---- routing + dispatch (k_route.hip) ----
 hipError_t launch_hold(hipStream_t s, uint32_t microseconds);
+hipError_t launch_route_sum(Prof *p, hipStream_t s, const float *parts, uint32_t nsplit,
+                            const float *bias, uint32_t experts, uint32_t k, int normalize,
+                            uint32_t tokens, float *logits, uint32_t *ids, float *weights);
+// Router product on the persistent MFMA GEMM: K split into `ksplit` ranges
+// (gemm_router_ksplit picks it for a partial buffer of `part_floats`); with
+// ksplit 1 `out` receives the logits (+ bias), else the partial sums
+// [ksplit, tokens, E] that launch_route_sum adds.
+uint32_t gemm_router_ksplit(const WDesc &r, uint32_t tokens, uint64_t part_floats);
+hipError_t launch_gemm_router(Prof *p, hipStream_t s, const WDesc &r, const uint16_t *xb16,
+                              uint32_t tokens, uint32_t ksplit, const float *bias, float *out);
 hipError_t launch_route(Prof *p, hipStream_t s, const float *logits, uint32_t experts, uint32_t k,
                         int normalize, uint32_t tokens, uint32_t *ids, float *weights);
 hipError_t launch_dispatch(Prof *p, hipStream_t s, const uint32_t *ids, uint32_t pairs,
