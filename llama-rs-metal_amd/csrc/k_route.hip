@@ -151,9 +151,126 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_place_kernel(
     }
 }
 
+// Single-pass dispatch: every block histograms all pairs (and those before
+// its chunk) in LDS, scans the counts over experts, and places its chunk of
+// kPlaceChunk pairs.  Within a wave, the rank of a pair among the earlier
+// lanes routed to the same expert comes from ballots over the bits of the
+// expert id; per-wave, per-expert running counts (LDS) carry it across the
+// wave's rounds and a per-expert prefix over the waves across the block.  So
+// perm is ordered by pair index within every expert, as in the two-pass path.
+constexpr int kPlaceThreads = 1024;
+constexpr int kPlaceWaves = kPlaceThreads / 64;
+constexpr int kPlaceRounds = 4;
+constexpr uint32_t kPlaceChunk = kPlaceWaves * kPlaceRounds * 64;
+constexpr int kHistLoads = 8;  // id loads in flight per thread while histogramming
+
+__global__ __launch_bounds__(kPlaceThreads) void dispatch_kernel(
+    const uint32_t *__restrict__ ids, uint32_t pairs, uint32_t E, uint32_t *__restrict__ counts,
+    uint32_t *__restrict__ offsets, uint32_t *__restrict__ perm, uint32_t *__restrict__ pos) {
+    extern __shared__ uint32_t sm[];
+    uint32_t *all = sm, *base = sm + E, *cw = sm + 2 * E;  // cw: [kPlaceWaves][E]
+    __shared__ uint32_t wsum[kPlaceWaves];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const uint32_t c0 = blockIdx.x * kPlaceChunk;
+    for (uint32_t i = tid; i < (2 + kPlaceWaves) * E; i += kPlaceThreads) sm[i] = 0u;
+    __syncthreads();
+    // counts of all pairs, and of the pairs before this chunk (kHistLoads
+    // loads issued before their atomics)
+    for (uint32_t b0 = 0; b0 < pairs; b0 += kPlaceThreads * kHistLoads) {
+        uint32_t v[kHistLoads];
+#pragma unroll
+        for (int i = 0; i < kHistLoads; i++) {
+            const uint32_t p = b0 + (uint32_t)(i * kPlaceThreads + tid);
+            v[i] = p < pairs ? ids[p] : E;
+        }
+#pragma unroll
+        for (int i = 0; i < kHistLoads; i++) {
+            if (v[i] < E) {
+                atomicAdd(&all[v[i]], 1u);
+                if (b0 + (uint32_t)(i * kPlaceThreads + tid) < c0) atomicAdd(&base[v[i]], 1u);
+            }
+        }
+    }
+    __syncthreads();
+    // exclusive scan over experts: thread t owns experts [t*per, t*per + per)
+    const uint32_t per = (E + kPlaceThreads - 1) / kPlaceThreads;
+    const uint32_t e0 = min(E, (uint32_t)tid * per), e1 = min(E, e0 + per);
+    uint32_t part = 0;
+    for (uint32_t e = e0; e < e1; e++) part += all[e];
+    uint32_t incl = part;
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t v = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += v;
+    }
+    if (lane == 63) wsum[wv] = incl;
+    __syncthreads();
+    uint32_t run = incl - part, total = 0;
+    for (int w = 0; w < kPlaceWaves; w++) {
+        if (w < wv) run += wsum[w];
+        total += wsum[w];
+    }
+    for (uint32_t e = e0; e < e1; e++) {
+        const uint32_t c = all[e];
+        if (blockIdx.x == 0) {
+            counts[e] = c;
+            offsets[e] = run;
+        }
+        base[e] += run;
+        run += c;
+    }
+    if (blockIdx.x == 0 && tid == 0) offsets[E] = total;
+    // ranks inside this chunk: wave wv takes pairs c0 + 64*(kPlaceRounds*wv + r) + lane
+    const int bits = 32 - __clz((int)E);  // distinguishes 0..E (E marks an absent pair)
+    const uint64_t below = (1ull << lane) - 1ull;
+    uint32_t pe[kPlaceRounds], pr[kPlaceRounds];
+#pragma unroll
+    for (int r = 0; r < kPlaceRounds; r++) {
+        const uint32_t p = c0 + 64u * (kPlaceRounds * wv + r) + lane;
+        uint32_t e = p < pairs ? ids[p] : E;
+        if (e > E) e = E;
+        uint64_t same = ~0ull;
+        for (int b = 0; b < bits; b++) {
+            const bool bit = (e >> b) & 1u;
+            const uint64_t m = __ballot(bit);
+            same &= bit ? m : ~m;
+        }
+        const uint32_t c = e < E ? cw[wv * E + e] : 0u;
+        // the group's last lane advances the running count (a wave's LDS
+        // operations execute in order, so every lane above read the old value)
+        if (e < E && (same >> lane) == 1ull) cw[wv * E + e] = c + (uint32_t)__popcll(same);
+        pe[r] = e;
+        pr[r] = c + (uint32_t)__popcll(same & below);
+    }
+    __syncthreads();
+    for (uint32_t e = tid; e < E; e += kPlaceThreads) {
+        uint32_t acc = 0;
+        for (int w = 0; w < kPlaceWaves; w++) {
+            const uint32_t t = cw[w * E + e];
+            cw[w * E + e] = acc;
+            acc += t;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kPlaceRounds; r++) {
+        if (pe[r] < E) {
+            const uint32_t p = c0 + 64u * (kPlaceRounds * wv + r) + lane;
+            const uint32_t q = base[pe[r]] + cw[wv * E + pe[r]] + pr[r];
+            perm[q] = p;
+            pos[p] = q;
+        }
+    }
+}
+
 hipError_t launch_dispatch(Prof *p, hipStream_t s, const uint32_t *ids, uint32_t pairs,
                            uint32_t experts, uint32_t *counts, uint32_t *offsets, uint32_t *perm,
                            uint32_t *pos) {
+    const size_t lds = (size_t)(2 + kPlaceWaves) * experts * sizeof(uint32_t);
+    if (lds <= 48 * 1024) {
+        const uint32_t nb = pairs ? (pairs + kPlaceChunk - 1) / kPlaceChunk : 1u;
+        return launch_kernel(p, "dispatch", dispatch_kernel, dim3(nb), dim3(kPlaceThreads), lds, s,
+                             ids, pairs, experts, counts, offsets, perm, pos);
+    }
     const uint32_t zb = (experts + kDispThreads - 1) / kDispThreads;
     hipError_t e = launch_kernel(p, "dispatch_zero", zero_u32_kernel, dim3(zb), dim3(kDispThreads), 0,
                                  s, counts, experts);
