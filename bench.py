@@ -13,6 +13,10 @@ step, every step on a fresh N(0,1) token.  Steps are captured into a HIP graph
 of 64 steps and replayed; the timed region is bracketed by stream
 synchronisation (hipEvents on the library's stream measure it).
 
+A third leg runs config 5: the 48-layer MoE-only stack (RMSNorm, MoE block,
+residual) at the config-2 shapes with 2-bit g32 and 8-bit g128 experts, 256
+decode steps each (skip with --no-stack).
+
 Output: one JSON line (see the driver contract) with the dominant kernel's
 roofline (algorithmic bytes / its hipEvent-measured average duration) and the
 CPU oracle timed on this host's cores.
@@ -138,6 +142,69 @@ def bench_prefill(gpu, iters=10):
     }
 
 
+# ---- config 5: 48-layer MoE-only stack (RMSNorm, MoE block, residual) ----
+STACK_LAYERS, STACK_STEPS, STACK_CHUNK = 48, 256, 8
+STACK_VARIANTS = {"2bit_g32": (2, 32), "8bit_g128": (8, 128)}
+
+
+def bench_stack(gpu, variant):
+    """Config 5: 256 decode steps at batch 1, each a fresh N(0,1) hidden state
+    through 48 layers of RMSNorm -> MoE block (config-2 shapes) -> residual.
+    The routed and shared expert weights of one seeded random layer are
+    uploaded 48 times (48 distinct HBM copies, all cold for the step); the
+    routers (F32) and norm weights are distinct per layer."""
+    bits, group = STACK_VARIANTS[variant]
+    s = 700 * 100 + bits
+    ex = [Tensor.affine(d, *synth.random_affine(s + i, int(np.prod(d)), bits, group, BF16), bits, group,
+                        BF16)
+          for i, d in enumerate(([H, FF, E], [H, FF, E], [FF, H, E]))]
+    sh = [Tensor.affine(d, *synth.random_affine(s + 3 + i, int(np.prod(d)), bits, group, BF16), bits,
+                        group, BF16)
+          for i, d in enumerate(([H, FFS], [H, FFS], [FFS, H]))]
+    sgate = Tensor.dense([H], synth.normal(s + 6, H, 0.0, 0.02))
+    layers, norms = [], []
+    for l in range(STACK_LAYERS):
+        router = Tensor.dense([H, E], synth.normal(s + 10 + l, H * E, 0.0, 0.02))
+        w = [gpu.weight_tensor(t) for t in [router, *ex]]
+        layers.append(BlockWeights(w[0], w[1], w[2], w[3], K, True,
+                                   tuple(gpu.weight_tensor(t) for t in sh), gpu.weight_tensor(sgate)))
+        norms.append(gpu.upload((1.0 + 0.1 * synth.normal(s + 100 + l, H)).astype(np.float32)))
+    resident = gpu.allocated_bytes()
+    log(f"[bench] config-5 {variant}: {STACK_LAYERS} layers resident ({resident / 1e9:.1f} GB on the GPU)")
+    xs = gpu.upload(synth.normal(s + 200, STACK_CHUNK * H))
+    hs = gpu.zeros(STACK_CHUNK * H)
+    ws = gpu.zeros(layers[0].workspace_elems(1))
+
+    def step(b, j):
+        h = hs.view(j * H, H)
+        b.copy(xs.view(j * H, H), h)
+        for l in range(STACK_LAYERS):
+            b.moe_block(layers[l], h, h, 1, ws, norm_weight=norms[l], norm_eps=1e-6, residual=True)
+
+    cap = gpu.capture()
+    with cap as b:
+        for j in range(STACK_CHUNK):
+            step(b, j)
+    with gpu.batch() as b:
+        b.graph(cap.graph)
+    with gpu.batch() as b:
+        for _ in range(STACK_STEPS // STACK_CHUNK):
+            b.graph(cap.graph)
+    per_token = b.seconds / STACK_STEPS
+    mat = lambda i, o: o * i * bits // 8 + 2 * (o * i // group) * 2
+    token_bytes = STACK_LAYERS * ((K + 1) * (2 * mat(H, FF) + mat(FF, H)) + H * E * 4 + H * 4)
+    del layers, norms
+    expert_bytes = STACK_LAYERS * (K + 1) * (2 * mat(H, FF) + mat(FF, H))
+    return {"variant": variant, "layers": STACK_LAYERS, "steps": STACK_STEPS,
+            "expert_bytes_per_token": expert_bytes,
+            "us_per_token": round(per_token * 1e6, 2), "tokens_per_s": round(1.0 / per_token, 1),
+            "us_per_layer": round(per_token * 1e6 / STACK_LAYERS, 3),
+            "bytes_per_token": token_bytes,
+            "achieved_GBps": round(token_bytes / per_token / 1e9, 1),
+            "hbm_frac": round(token_bytes / per_token / HBM_PEAK, 4),
+            "weights": "one seeded random expert set uploaded 48 times; distinct F32 routers and norm weights"}
+
+
 def cpu_baseline(tensors, budget_s):
     """The C oracle (single thread) on the same layer, bounded sample."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -209,6 +276,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-stack", action="store_true")
     ap.add_argument("--traffic-probe", choices=["decode", "prefill"], default=None,
                     help="short eager workload for rocprofv3 --pmc runs (no timing output)")
     args = ap.parse_args()
@@ -329,6 +397,13 @@ def main():
         result["prefill"] = bench_prefill(gpu)
         log(f"[bench] prefill: {result['prefill']['ms_per_layer']} ms/layer, "
             f"{result['prefill']['achieved_TFLOPs']} TFLOP/s")
+    if not args.no_stack:
+        result["stack"] = []
+        for v in STACK_VARIANTS:
+            r = bench_stack(gpu, v)
+            log(f"[bench] config-5 {v}: {r['us_per_token']} us/token over {STACK_LAYERS} layers, "
+                f"{r['achieved_GBps']} GB/s")
+            result["stack"].append(r)
     if not args.no_cpu:
         log("[bench] timing the CPU oracle")
         result["cpu_baseline"] = cpu_baseline(host0, args.cpu_seconds)

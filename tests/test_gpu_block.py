@@ -190,11 +190,23 @@ def test_config3_mixed_precision_hot_set(gpu, c3, T):
 
 
 # ------------------------------------------------------------------ config 5 --
+@pytest.fixture(scope="module")
+def c5(gpu):
+    """Config-5 layers by variant, generated and uploaded once per module."""
+    cache = {}
+
+    def get(variant):
+        if variant not in cache:
+            blk = config5(variant)
+            cache[variant] = (blk, blk.upload(gpu))
+        return cache[variant]
+    return get
+
+
 @pytest.mark.parametrize("variant", ["2bit", "8bit"])
-def test_config5_layer_norm_residual(gpu, variant):
+def test_config5_layer_norm_residual(gpu, c5, variant):
     print(f"[case] config5 {variant}", flush=True)
-    blk = config5(variant)
-    bw = blk.upload(gpu)
+    blk, bw = c5(variant)
     nw = (1.0 + 0.1 * synth.normal(3000, 2048)).astype(np.float32)
     x = synth.normal(3001, 2048).reshape(1, 2048)
     got = run_block(gpu, bw, x, 1, PATH_AUTO, norm_w=nw, residual=True)
@@ -202,6 +214,31 @@ def test_config5_layer_norm_residual(gpu, variant):
     got_g = run_block(gpu, bw, x, 1, PATH_GROUPED, norm_w=nw, residual=True)
     assert np.array_equal(got[2], got_g[2])
     assert rel_max_err(got_g[0], got[0]) <= F32_TOL
+
+
+@pytest.mark.parametrize("variant", ["2bit", "8bit"])
+def test_config5_stack_chain(gpu, c5, variant):
+    """Three layers of the config-5 stack (RMSNorm -> MoE block -> residual),
+    chained in place on the GPU in one batch, against the oracle's stack
+    (orc_moe_stack) on the same input.  The layers share the expert weights
+    and differ in their norm weights, so every layer routes differently."""
+    print(f"[case] config5 stack {variant}", flush=True)
+    blk, bw = c5(variant)
+    nws = [(1.0 + 0.3 * synth.normal(3100 + l, 2048)).astype(np.float32) for l in range(3)]
+    x = synth.normal(3200, 2048).reshape(1, 2048)
+    h = gpu.upload(x)
+    ws = gpu.zeros(bw.workspace_elems(1))
+    nbs = [gpu.upload(n) for n in nws]
+    with gpu.batch() as b:
+        for nb in nbs:
+            b.moe_block(bw, h, h, 1, ws, norm_weight=nb, norm_eps=1e-6, residual=True)
+    got = gpu.read(h).reshape(1, 2048)
+    ref = oracle.moe_stack([blk.spec()] * 3, nws, 1e-6, x, 1)
+    err = rel_max_err(got, ref)
+    print(f"[case] config5 stack {variant} rel err {err:.3e}", flush=True)
+    assert err <= F32_TOL
+    for buf in (h, ws, *nbs):
+        gpu.release(buf)
 
 
 def test_in_place_residual_stream(gpu, c2):
