@@ -241,6 +241,35 @@ def test_config5_stack_chain(gpu, c5, variant):
         gpu.release(buf)
 
 
+def test_mlx_checkpoint_layer(gpu, tmp_path):
+    """A synthetic MLX checkpoint (sharded SafeTensors, 8-bit router, 4-bit
+    experts and shared expert, bf16 norm) loaded by hip_backend.mlx and run
+    through moe_block with its norm and the residual, decode and batched."""
+    import oracle as orc
+    from hip_backend.mlx import MoeCheckpoint
+    from mlx_fixture import make_checkpoint
+    make_checkpoint(str(tmp_path), layers=1, shards=2)
+    ck = MoeCheckpoint(str(tmp_path))
+    bw, nb = ck.upload(gpu, 0)
+    L = ck.layers[0]
+
+    class Spec:
+        router = L["router"]
+
+        @staticmethod
+        def spec():
+            return orc.MoeSpec(L["router"], L["gate"], L["up"], L["down"], ck.experts_used,
+                               ck.normalize, (L["shared_gate"], L["shared_up"], L["shared_down"]),
+                               L["shared_gate_inp"])
+    nw = gpu.read(nb)
+    for T in (1, 3):
+        print(f"[case] mlx checkpoint T={T}", flush=True)
+        x = synth.normal(3300 + T, T * 256).reshape(T, 256)
+        got = run_block(gpu, bw, x, T, PATH_AUTO, norm_w=nw, residual=True)
+        check_against_oracle(Spec, x, got, norm_w=nw, residual=True)
+    gpu.release(nb)
+
+
 def test_in_place_residual_stream(gpu, c2):
     blk, bw = c2
     x = synth.normal(3100, 2048)
