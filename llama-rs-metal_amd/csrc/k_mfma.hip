@@ -270,6 +270,44 @@ __global__ __launch_bounds__(64) void to_bf16_kernel(const float *__restrict__ x
     }
 }
 
+// Same conversion with 8 elements per thread (two 16-byte loads, one 16-byte
+// bf16 store), a block of up to 256 threads per row; h % 8 == 0.
+__global__ __launch_bounds__(256) void to_bf16v_kernel(const float *__restrict__ x,
+                                                      const float *__restrict__ norm_w, float eps,
+                                                      uint32_t h, uint16_t *__restrict__ y,
+                                                      float *__restrict__ xn) {
+    __shared__ float part[4];
+    const uint64_t row = blockIdx.x;
+    const float *xr = x + row * h;
+    float inv = 1.f;
+    if (norm_w) {
+        float ss = 0.f;
+        for (uint32_t i = threadIdx.x; i < h; i += blockDim.x) ss += xr[i] * xr[i];
+        ss = wave_sum(ss);
+        if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        ss = 0.f;
+        for (uint32_t w = 0; w < blockDim.x / 64; w++) ss += part[w];
+        inv = 1.0f / sqrtf(ss / (float)h + eps);
+    }
+    for (uint32_t i = 8 * threadIdx.x; i < h; i += 8 * blockDim.x) {
+        const float4 a = *reinterpret_cast<const float4 *>(xr + i);
+        const float4 b = *reinterpret_cast<const float4 *>(xr + i + 4);
+        float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        if (norm_w) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = v[j] * inv * norm_w[i + j];
+            if (xn) {
+                float4 *d = reinterpret_cast<float4 *>(xn + row * h + i);
+                d[0] = make_float4(v[0], v[1], v[2], v[3]);
+                d[1] = make_float4(v[4], v[5], v[6], v[7]);
+            }
+        }
+        *reinterpret_cast<u32x4m *>(y + row * h + i) =
+            u32x4m{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]), pack_bf16(v[6], v[7])};
+    }
+}
+
 // Tile list: M-tiles of `tm` positions over every non-empty expert segment.
 __global__ __launch_bounds__(64) void tile_schedule_kernel(const uint32_t *__restrict__ offsets,
                                                            uint32_t E, uint32_t tm,
@@ -355,6 +393,13 @@ struct MfmaLaunch {
 
 hipError_t launch_to_bf16(Prof *p, hipStream_t s, const float *x, const float *norm_w, float eps,
                           uint32_t tokens, uint32_t h, uint16_t *y, float *xn) {
+    const bool vec = h % 8 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y) |
+                                     reinterpret_cast<uintptr_t>(xn)) & 15u) == 0;
+    if (vec) {
+        const uint32_t threads = h / 8 < 256 ? ((h / 8 + 63) / 64) * 64 : 256;
+        return launch_kernel(p, "to_bf16", to_bf16v_kernel, dim3(tokens), dim3(threads), 0, s, x,
+                             norm_w, eps, h, y, xn);
+    }
     return launch_kernel(p, "to_bf16", to_bf16_kernel, dim3(tokens), dim3(64), 0, s, x, norm_w, eps,
                          h, y, xn);
 }
@@ -385,9 +430,73 @@ hipError_t launch_mfma_experts(Prof *p, hipStream_t s, const WDesc &gate, const 
     return launch_grouped_gemm(p, s, 1, down, down, act16, perm, offsets, tiles, ntiles, route_w, k, y16);
 }
 
+// Same combine with 8 columns per thread (16-byte row loads, all K rows of a
+// group of up to 8 issued before the accumulation; the sum still runs over k
+// ascending).  One block of h/8 threads per token; h % 8 == 0.
+constexpr uint32_t kCombKMax = 8;
+__global__ __launch_bounds__(256) void combine16v_kernel(const uint16_t *__restrict__ y16,
+                                                         const uint32_t *__restrict__ pos,
+                                                         const float *__restrict__ wts, uint32_t K,
+                                                         const float *__restrict__ sh_out,
+                                                         const float *__restrict__ sh_gate,
+                                                         const float *__restrict__ resid,
+                                                         float *__restrict__ out, uint32_t h) {
+    const uint32_t t = blockIdx.y;
+    const uint32_t i = 8 * (blockIdx.x * blockDim.x + threadIdx.x);
+    if (i >= h) return;
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] = 0.f;
+    // mix (elementwise.metal:47-57): sum over k ascending of w[k] * y_k
+    for (uint32_t k0 = 0; k0 < K; k0 += kCombKMax) {
+        const uint32_t n = min(kCombKMax, K - k0);
+        u32x4m r[kCombKMax];
+        float w[kCombKMax];
+#pragma unroll
+        for (uint32_t k = 0; k < kCombKMax; k++) {
+            if (k < n) {
+                const uint64_t pk = (uint64_t)t * K + k0 + k;
+                r[k] = *reinterpret_cast<const u32x4m *>(y16 + (uint64_t)pos[pk] * h + i);
+                w[k] = wts[pk];
+            }
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kCombKMax; k++) {
+            if (k < n) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    v[2 * q] += bf16_lo(r[k][q]) * w[k];
+                    v[2 * q + 1] += bf16_hi(r[k][q]) * w[k];
+                }
+            }
+        }
+    }
+    const uint64_t o = (uint64_t)t * h + i;
+    if (sh_out) {
+        const float d = 1.0f + expf(-sh_gate[t]);
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = v[j] + sh_out[o + j] / d;
+    }
+    if (resid) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = resid[o + j] + v[j];
+    }
+    float4 *dst = reinterpret_cast<float4 *>(out + o);
+    dst[0] = make_float4(v[0], v[1], v[2], v[3]);
+    dst[1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+
 hipError_t launch_combine16(Prof *p, hipStream_t s, const uint16_t *y16, const uint32_t *pos,
                             const float *wts, uint32_t k, const float *sh_out, const float *sh_gate,
                             const float *resid, float *out, uint32_t tokens, uint32_t h) {
+    const bool vec = h % 8 == 0 && (reinterpret_cast<uintptr_t>(y16) & 15u) == 0 &&
+                     (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
+    if (vec) {
+        const uint32_t threads = h / 8 < 256 ? ((h / 8 + 63) / 64) * 64 : 256;
+        dim3 grid((h / 8 + threads - 1) / threads, tokens);
+        return launch_kernel(p, "combine16", combine16v_kernel, grid, dim3(threads), 0, s, y16, pos,
+                             wts, k, sh_out, sh_gate, resid, out, h);
+    }
     dim3 grid((h / 2 + 255) / 256, tokens);
     return launch_kernel(p, "combine16", combine16_kernel, grid, dim3(256), 0, s, y16, pos, wts, k,
                          sh_out, sh_gate, resid, out, h);
