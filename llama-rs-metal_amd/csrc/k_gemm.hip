@@ -64,7 +64,6 @@ constexpr int kAChunksPerRow = kTK * 2 / 16;  // 16-byte chunks of one A row per
 constexpr int kAChunks = kTM * kAChunksPerRow / kThreads;  // A chunks one thread stages per step
 constexpr int kARowsPerPass = kThreads / kAChunksPerRow;   // A rows one pass covers
 constexpr int kXcds = 8;
-constexpr bool kInterleave = false;  // spread dequant VALU and LDS reads between the MFMAs
 
 enum { GATEUP = 1, DOWN = 2, ROUTER = 3 };
 static_assert(kNT % 2 == 0, "gate/up columns pair up inside a wave");
@@ -115,7 +114,6 @@ struct Args {
     const uint32_t *offsets;   // [E+1] segment offsets
     const uint32_t *tiles;     // [2*max_tiles] (expert, first position)
     const uint32_t *ntiles;    // number of valid M-tiles (device)
-    const float *route_w;      // DOWN: routing weight of each pair [T*K]
     uint16_t *out;             // GATEUP: act16 [P, ff]; DOWN: y16 [P, h]
     float *out_f32;            // ROUTER: logits [T, E] (ksplit 1) or partials [ksplit, T, E]
     const float *bias;         // ROUTER with ksplit 1: optional logit bias [T, E]
@@ -356,18 +354,6 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void grouped_gemm_kernel(Ar
                 }
             }
             store_step(ST ^ 1, ST ^ 1);  // may interleave with the MFMAs above
-            if constexpr (kInterleave) {
-                // per MFMA: one fragment read and a share of the dequantisation,
-                // so the VALU and LDS work issues in the MFMAs' shadow
-                constexpr int kMfmas = kMT * kNT * (kTK / 16);
-#pragma unroll
-                for (int i = 0; i < kMfmas; i++) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-                    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
-                }
-                __builtin_amdgcn_sched_group_barrier(0x200, 16, 0);    // DS writes
-            }
             __syncthreads();
         };
         load_step(0, kbeg);
@@ -471,8 +457,8 @@ struct SetLds {
 
 hipError_t launch_grouped_gemm(Prof *p, hipStream_t s, int down, const WDesc &w, const WDesc &w2,
                                const uint16_t *a_rows, const uint32_t *perm, const uint32_t *offsets,
-                               const uint32_t *tiles, const uint32_t *ntiles, const float *route_w,
-                               uint32_t k, uint16_t *out) {
+                               const uint32_t *tiles, const uint32_t *ntiles, uint32_t k,
+                               uint16_t *out) {
     gemm::Args a{};
     a.w = w;
     a.w2 = w2;
@@ -481,7 +467,6 @@ hipError_t launch_grouped_gemm(Prof *p, hipStream_t s, int down, const WDesc &w,
     a.offsets = offsets;
     a.tiles = tiles;
     a.ntiles = ntiles;
-    a.route_w = route_w;
     a.out = out;
     a.k = k;
     const uint32_t blocks = gemm_blocks();

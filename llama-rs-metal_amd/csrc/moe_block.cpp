@@ -190,7 +190,7 @@ moe_status run_grouped(moe_gpu *g, const moe_block_weights *w, const Dims &d, co
 
 bool mfma_path_ok(const moe_block_weights *w, const Dims &d) {
     const WDesc G = wdesc(w->gate), U = wdesc(w->up), D = wdesc(w->down);
-    return mfma_supported(G) && mfma_supported(U) && mfma_supported(D) && G.bits == U.bits &&
+    return gemm_supported(G) && gemm_supported(U) && gemm_supported(D) && G.bits == U.bits &&
            G.type == U.type && d.h % 128 == 0 && d.ff % 128 == 0;
 }
 
@@ -229,17 +229,13 @@ moe_status run_mfma(moe_gpu *g, const moe_block_weights *w, const Dims &d, const
             TRY(launch_route(p, s, logits, E, K, w->normalize ? 1 : 0, (uint32_t)T, ids, wts));
         }
     } else {
-        if (mfma_supported(R)) {
-            TRY(launch_mfma_router(p, s, R, xb16, (uint32_t)T, bias, logits));
-        } else {
-            TRY(launch_gemv(p, s, R, xin, 0, nullptr, 1, logits, (uint32_t)T));
-            if (bias) TRY(launch_add(p, s, logits, bias, logits, T * d.E));
-        }
+        TRY(launch_gemv(p, s, R, xin, 0, nullptr, 1, logits, (uint32_t)T));
+        if (bias) TRY(launch_add(p, s, logits, bias, logits, T * d.E));
         TRY(launch_route(p, s, logits, E, K, w->normalize ? 1 : 0, (uint32_t)T, ids, wts));
     }
     TRY(launch_dispatch(p, s, ids, (uint32_t)(T * K), E, counts, offsets, perm, pos));
     TRY(launch_mfma_experts(p, s, wdesc(w->gate), wdesc(w->up), wdesc(w->down), xb16, offsets, perm,
-                            wts, K, (uint32_t)(T * K), tiles, ntiles, act16, y16));
+                            K, tiles, ntiles, act16, y16));
     const float *so = nullptr, *sgv = nullptr;
     if (w->has_shared) {
         float *sg = ws + L.sh_act, *su = ws + L.sh_up, *sout = ws + L.sh_out, *sgt = ws + L.sh_gate;
