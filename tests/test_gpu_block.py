@@ -303,6 +303,23 @@ def test_config4_prefill_mfma_zipf(gpu, c4):
     assert counts.max() > 8 * counts.mean()  # the Zipf skew is realised
 
 
+@pytest.mark.parametrize("T", [33, 32768])
+def test_config4_prefill_sizes(gpu, c4, T):
+    """Prefill at a ragged token count (partial M-tiles everywhere) and at
+    32768 tokens, where the router GEMM runs unsplit (its tiles alone fill the
+    grid), so it adds the bias itself and the routing reads plain logits; the
+    dispatch places 262144 pairs."""
+    blk, bw = c4
+    print(f"[case] config4 prefill T={T}", flush=True)
+    x = synth.normal(4300 + T, T * 2048).reshape(T, 2048)
+    bias = zipf_bias(T, 128, seed=5)
+    got = run_block(gpu, bw, x, T, PATH_MFMA, bias=bias)
+    sample = sorted(set(list(range(0, T, max(1, T // 12))) + [T - 1]))
+    err = check_against_oracle(blk, x, got, tokens=sample, bias=bias, tol=BF16_TOL,
+                               logit_tol=BF16_TOL)
+    print(f"[case] config4 T={T} rel err {err:.3e}", flush=True)
+
+
 def test_mfma_path_with_shared_expert(gpu, c2):
     blk, bw = c2
     T = 256
