@@ -20,6 +20,16 @@
 // their range together, so the tiles that share an expert's weights and a
 // segment's activation rows run side by side on one L2.
 //
+// Two kernels share that schedule.  affine_gemm_kernel (GATEUP and DOWN over
+// 2/4/8-bit affine weights, the prefill hot path) keeps the weights out of
+// LDS: each of its two waves owns all kTM rows and 64 weight rows of the
+// tile, loads its own codes into registers and dequantises them straight
+// into MFMA operands (every weight value once per block), while the A tile
+// reaches LDS by buffer DMA (buffer_load_dwordx4 ... lds), 16-byte chunks
+// XOR-swizzled so the fragment reads are conflict-free.  Four such blocks
+// share a CU.  grouped_gemm_kernel (ROUTER, dense weights, and tensors whose
+// offsets exceed 32 bits) stages both operands through LDS:
+//
 // Per 64-wide K step, double-buffered in LDS: the block's threads load the
 // A tile (kTM rows x 128 bytes of bf16, rows gathered through perm for
 // GATEUP) and the B tile (128 weight rows x 64 codes, dequantised once per
@@ -412,16 +422,251 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void grouped_gemm_kernel(Ar
     }
 }
 
+// ------------------------------------------------------ affine_gemm ----
+constexpr int kAfThreads = 128;     // two waves
+constexpr int kAfBlocksPerCu = 4;   // 4 x 32 KiB of LDS, 2 waves per SIMD
+constexpr int kAfNT = 2;            // 32-row weight tiles per wave
+constexpr int kAfATile = kTM * kTK * 2;  // one A stage: kTM rows x 128 bytes
+constexpr int kRsrcWord3 = 0x00020000;   // gfx9 buffer resource: raw, untyped
+
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, 0xffffffff, kRsrcWord3);
+}
+// Position of 16-byte chunk c of A-tile row r inside the row: chunks are
+// XOR-permuted so the 32 rows one fragment read touches spread over the banks.
+__device__ __forceinline__ uint32_t a_chunk(uint32_t r, uint32_t c) { return c ^ ((r ^ (r >> 3)) & 7u); }
+
+// One lane's codes (32 consecutive K values) of its kAfNT weight rows for one
+// K step, with the raw bits of their groups' scales and biases.
+template <int BITS>
+struct AfStage {
+    uint32_t w[kAfNT][BITS];
+    uint32_t s[kAfNT], b[kAfNT];
+};
+
+// The 8 codes k = 8j .. 8j + 7 of a lane's 32, as floats.
+template <int BITS>
+__device__ __forceinline__ void codes8(const uint32_t *w, int j, float *c) {
+    if constexpr (BITS == 4) {
+        codes_f32<4>(w[j], c);
+    } else if constexpr (BITS == 8) {
+        codes_f32<8>(w[2 * j], c);
+        codes_f32<8>(w[2 * j + 1], c + 4);
+    } else {
+        float t[16];
+        codes_f32<2>(w[j >> 1] >> (16 * (j & 1)), t);
+#pragma unroll
+        for (int i = 0; i < 8; i++) c[i] = t[i];
+    }
+}
+
+// One work item with NS live 32-row slices of A (rows past the segment end
+// are neither loaded nor multiplied).  Wave wv owns weight rows
+// [64 wv, 64 wv + 64) of the N-tile (GATEUP: 32 gate rows and the 32 up rows
+// of the same outputs); lane half h feeds K values 32h + 8j + [0, 8) at MFMA
+// step j to both operands.
+template <int MODE, int BITS, int T, int NS>
+__device__ __forceinline__ void affine_item(const Args &a, uint8_t *abuf, uint32_t nt, uint32_t e,
+                                            uint32_t m0, uint32_t seg_end, int lane, int wv) {
+    const int h = lane >> 5, l32 = lane & 31;
+    const uint32_t in = a.w.in, out = a.w.out, nk = in / kTK;
+    constexpr int ND = 2 * NS;  // DMA instructions per wave and step (8 rows each)
+    // A: DMA instruction i of wave wv fills tile rows 16i + 8wv .. +7, lane
+    // (row, chunk position) = (lane / 8, lane % 8); byte offsets below 2^32
+    // (checked on the host).  Rows past the segment re-read its first row.
+    const uint32_t drow = 8 * wv + (lane >> 3), dpos = lane & 7;
+    uint32_t aoff[ND];
+#pragma unroll
+    for (int i = 0; i < ND; i++) {
+        const uint32_t r = 16 * i + drow;
+        uint32_t pos = m0 + r;
+        if (pos >= seg_end) pos = m0;
+        const uint32_t src = MODE == GATEUP ? a.perm[pos] / a.k : pos;
+        aoff[i] = src * in * 2 + (a_chunk(r, dpos) << 4);
+    }
+    // B: weight row n of tile t; rows past `out` read row 0 (never stored)
+    uint32_t el0[kAfNT];  // element index of the lane's codes at K step 0 (< 2^32, host-checked)
+#pragma unroll
+    for (int t = 0; t < kAfNT; t++) {
+        uint32_t n = MODE == GATEUP ? nt * (kTN / 2) + 32 * wv + l32 : nt * kTN + 64 * wv + 32 * t + l32;
+        if (n >= out) n = 0;
+        el0[t] = (e * out + n) * in + 32 * h;
+    }
+    const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.a_rows);
+    const __amdgpu_buffer_rsrc_t rw[kAfNT] = {buffer_rsrc(a.w.data), buffer_rsrc(MODE == GATEUP ? a.w2.data : a.w.data)};
+    const __amdgpu_buffer_rsrc_t rs[kAfNT] = {buffer_rsrc(a.w.scales), buffer_rsrc(MODE == GATEUP ? a.w2.scales : a.w.scales)};
+    const __amdgpu_buffer_rsrc_t rb[kAfNT] = {buffer_rsrc(a.w.biases), buffer_rsrc(MODE == GATEUP ? a.w2.biases : a.w.biases)};
+    const uint32_t gshift = a.w.gshift;
+
+    f32x16 acc[NS][kAfNT];
+#pragma unroll
+    for (int s = 0; s < NS; s++)
+#pragma unroll
+        for (int t = 0; t < kAfNT; t++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[s][t][r] = 0.f;
+
+    auto dma = [&](uint32_t buf, uint32_t kb) {
+        uint8_t *dst = abuf + buf * kAfATile + 8 * wv * (kTK * 2);
+#pragma unroll
+        for (int i = 0; i < ND; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(dst + 16 * i * (kTK * 2)), 16, aoff[i],
+                                                     kb * (kTK * 2), 0, 0);
+    };
+    auto load_b = [&](AfStage<BITS> &st, uint32_t kb) {
+#pragma unroll
+        for (int t = 0; t < kAfNT; t++) {
+            const uint32_t vo = el0[t] / (8 / BITS), so = kb * (8 * BITS);
+            if constexpr (BITS == 2) {
+                const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rw[t], vo, so, 0);
+                st.w[t][0] = v[0];
+                st.w[t][1] = v[1];
+            } else {
+#pragma unroll
+                for (int i = 0; i < BITS / 4; i++) {
+                    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rw[t], vo + 16 * i, so, 0);
+                    st.w[t][4 * i] = v[0];
+                    st.w[t][4 * i + 1] = v[1];
+                    st.w[t][4 * i + 2] = v[2];
+                    st.w[t][4 * i + 3] = v[3];
+                }
+            }
+            const uint32_t g = (el0[t] + kb * kTK) >> gshift;  // 32 codes lie in one group
+            if constexpr (T == 0) {
+                st.s[t] = __builtin_amdgcn_raw_buffer_load_b32(rs[t], g * 4, 0, 0);
+                st.b[t] = __builtin_amdgcn_raw_buffer_load_b32(rb[t], g * 4, 0, 0);
+            } else {
+                st.s[t] = __builtin_amdgcn_raw_buffer_load_b16(rs[t], g * 2, 0, 0);
+                st.b[t] = __builtin_amdgcn_raw_buffer_load_b16(rb[t], g * 2, 0, 0);
+            }
+        }
+    };
+    auto compute = [&](const uint8_t *cur, const AfStage<BITS> &sc) {
+        float sf[kAfNT], bf[kAfNT];
+#pragma unroll
+        for (int t = 0; t < kAfNT; t++) {
+            sf[t] = BStage<BITS, T>::scalar(sc.s[t]);
+            bf[t] = BStage<BITS, T>::scalar(sc.b[t]);
+        }
+#pragma unroll
+        for (int j = 0; j < kTK / 16; j++) {
+            bf16x8 bfr[kAfNT], afr[NS];
+#pragma unroll
+            for (int s = 0; s < NS; s++) {
+                const uint32_t R = 32 * s + l32;
+                afr[s] = *reinterpret_cast<const bf16x8 *>(cur + R * (kTK * 2) + (a_chunk(R, 4 * h + j) << 4));
+            }
+#pragma unroll
+            for (int t = 0; t < kAfNT; t++) {
+                // w = code * scale + bias in F32, rounded to bf16
+                float c[8];
+                codes8<BITS>(sc.w[t], j, c);
+                u32x4 o;
+#pragma unroll
+                for (int i = 0; i < 4; i++) o[i] = pack_bf16(fmaf(c[2 * i], sf[t], bf[t]), fmaf(c[2 * i + 1], sf[t], bf[t]));
+                bfr[t] = __builtin_bit_cast(bf16x8, o);
+            }
+#pragma unroll
+            for (int s = 0; s < NS; s++)
+#pragma unroll
+                for (int t = 0; t < kAfNT; t++)
+                    acc[s][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afr[s], bfr[t], acc[s][t], 0, 0, 0);
+        }
+    };
+    // Step kb: wait for this wave's DMA into stage kb & 1 and its weight loads
+    // (issued one step earlier), then the barrier makes the other wave's DMA
+    // visible and retires both waves' reads of the other stage, which the
+    // DMA for kb + 1 then refills.  Past the last step the loads repeat step
+    // nk - 1 into the idle stage.
+    AfStage<BITS> bs0, bs1;
+    __builtin_amdgcn_s_waitcnt(0);  // the previous item's last DMA landed
+    __builtin_amdgcn_s_barrier();   // and both waves finished reading both stages
+    dma(0, 0);
+    load_b(bs0, 0);
+    auto step = [&](uint32_t kb, const AfStage<BITS> &sc, AfStage<BITS> &sn) {
+        __builtin_amdgcn_s_waitcnt(0);
+        __builtin_amdgcn_s_barrier();
+        const uint32_t kn = min(kb + 1, nk - 1);
+        dma((kb + 1) & 1, kn);
+        load_b(sn, kn);
+        compute(abuf + (kb & 1) * kAfATile, sc);
+    };
+    for (uint32_t kb = 0; kb < nk; kb += 2) {  // nk is even (in % 128 == 0)
+        step(kb, bs0, bs1);
+        step(kb + 1, bs1, bs0);
+    }
+    // acc[s][t][r] = C[32 s + 8 (r / 4) + 4 h + r % 4][this wave's column 32 t + l32]
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const uint32_t pos = m0 + 32 * s + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (pos >= seg_end) continue;
+            if constexpr (MODE == GATEUP) {
+                const uint32_t j = nt * (kTN / 2) + 32 * wv + l32;
+                if (j < out) {
+                    // activation (elementwise.metal:8-17), base-2 exponential and
+                    // hardware reciprocal; the result is rounded to bf16
+                    const float g = acc[s][0][r], u = acc[s][1][r];
+                    const float act = g * __builtin_amdgcn_rcpf(1.0f + exp_fast(-g)) * u;
+                    a.out[(uint64_t)pos * out + j] = (uint16_t)(pack_bf16(act, 0.f) & 0xffffu);
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < kAfNT; t++) {
+                    const uint32_t n = nt * kTN + 64 * wv + 32 * t + l32;
+                    if (n < out) a.out[(uint64_t)pos * out + n] = (uint16_t)(pack_bf16(acc[s][t][r], 0.f) & 0xffffu);
+                }
+            }
+        }
+    }
+}
+
+// Affine GATEUP / DOWN products: same persistent XCD-range schedule as
+// grouped_gemm_kernel, two waves per block, at most 256 VGPRs per lane so two
+// waves share a SIMD.
+template <int MODE, int BITS, int T>
+__global__ __attribute__((amdgpu_flat_work_group_size(kAfThreads, kAfThreads), amdgpu_waves_per_eu(2, 2)))
+void affine_gemm_kernel(Args a) {
+    static_assert(MODE == GATEUP || MODE == DOWN, "affine_gemm_kernel: expert products only");
+    static_assert(BITS == 2 || BITS == 4 || BITS == 8, "affine_gemm_kernel: affine weights only");
+    __shared__ __attribute__((aligned(16))) uint8_t abuf[2 * kAfATile];
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t items = *a.ntiles * a.n_tiles_n;
+    const uint32_t xcd = blockIdx.x % kXcds, q = blockIdx.x / kXcds, nq = gridDim.x / kXcds;
+    const uint32_t per_xcd = (items + kXcds - 1) / kXcds;
+    const uint32_t lo = xcd * per_xcd, hi = min(items, lo + per_xcd);
+    for (uint32_t item = lo + q; item < hi; item += nq) {
+        const uint32_t mt = item / a.n_tiles_n, nt = item % a.n_tiles_n;
+        const uint32_t e = a.tiles[2 * mt], m0 = a.tiles[2 * mt + 1];
+        const uint32_t seg_end = a.offsets[e + 1];
+        const uint32_t live = min(seg_end - m0, (uint32_t)kTM);
+        if (live > 96) affine_item<MODE, BITS, T, 4>(a, abuf, nt, e, m0, seg_end, lane, wv);
+        else if (live > 64) affine_item<MODE, BITS, T, 3>(a, abuf, nt, e, m0, seg_end, lane, wv);
+        else if (live > 32) affine_item<MODE, BITS, T, 2>(a, abuf, nt, e, m0, seg_end, lane, wv);
+        else affine_item<MODE, BITS, T, 1>(a, abuf, nt, e, m0, seg_end, lane, wv);
+    }
+}
+
 template <int MODE>
 struct Launch {
     Prof *p;
     hipStream_t s;
     const Args &a;
     uint32_t blocks;
+    bool affine;  // affine_gemm_kernel (affine_blocks blocks)
+    uint32_t affine_blocks;
     template <int BITS, int T>
     hipError_t operator()() {
-        return launch_kernel(p, MODE == DOWN ? "gemm_down" : MODE == ROUTER ? "gemm_router" : "gemm_gateup",
-                             grouped_gemm_kernel<MODE, BITS, T>, dim3(blocks), dim3(kThreads),
+        const char *name = MODE == DOWN ? "gemm_down" : MODE == ROUTER ? "gemm_router" : "gemm_gateup";
+        if constexpr (MODE != ROUTER && BITS != 0) {
+            if (affine)
+                return launch_kernel(p, name, affine_gemm_kernel<MODE, BITS, T>, dim3(affine_blocks),
+                                     dim3(kAfThreads), 0, s, a);
+        }
+        return launch_kernel(p, name, grouped_gemm_kernel<MODE, BITS, T>, dim3(blocks), dim3(kThreads),
                              kLdsBytes, s, a);
     }
 };
@@ -436,13 +681,21 @@ bool gemm_supported(const WDesc &w) {
 
 uint32_t gemm_tile_rows() { return gemm::kTM; }
 
-// Persistent grid: kBlocksPerCu blocks on every CU (a multiple of 8 so each
-// XCD gets the same number).
-static uint32_t gemm_blocks() {
+// Persistent grid: `per_cu` blocks on every CU (a multiple of 8 so each XCD
+// gets the same number).
+static uint32_t gemm_blocks(int per_cu = gemm::kBlocksPerCu) {
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) == hipSuccess)
         (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    return (uint32_t)((cus * gemm::kBlocksPerCu + 7) / 8 * 8);
+    return (uint32_t)((cus * per_cu + 7) / 8 * 8);
+}
+
+// affine_gemm_kernel addresses its operands with 32-bit buffer offsets.
+static bool affine_fits(const WDesc &w, uint64_t a_rows_n) {
+    if (w.bits == 0) return false;
+    const uint64_t elems = (uint64_t)w.experts * w.out * w.in;
+    const uint64_t groups = elems >> w.gshift;
+    return elems < (1ull << 32) && groups * 4 < (1ull << 32) && a_rows_n * w.in * 2 < (1ull << 32);
 }
 
 // Allows the kernel's dynamic LDS size (above the default per-launch limit).
@@ -456,9 +709,9 @@ struct SetLds {
 };
 
 hipError_t launch_grouped_gemm(Prof *p, hipStream_t s, int down, const WDesc &w, const WDesc &w2,
-                               const uint16_t *a_rows, const uint32_t *perm, const uint32_t *offsets,
-                               const uint32_t *tiles, const uint32_t *ntiles, uint32_t k,
-                               uint16_t *out) {
+                               const uint16_t *a_rows, uint64_t a_rows_n, const uint32_t *perm,
+                               const uint32_t *offsets, const uint32_t *tiles, const uint32_t *ntiles,
+                               uint32_t k, uint16_t *out) {
     gemm::Args a{};
     a.w = w;
     a.w2 = w2;
@@ -470,15 +723,18 @@ hipError_t launch_grouped_gemm(Prof *p, hipStream_t s, int down, const WDesc &w,
     a.out = out;
     a.k = k;
     const uint32_t blocks = gemm_blocks();
+    const bool affine = affine_fits(w, a_rows_n) && affine_fits(w2, a_rows_n) && w2.bits == w.bits &&
+                        w2.type == w.type && w2.gshift == w.gshift;
+    const uint32_t affine_blocks = gemm_blocks(gemm::kAfBlocksPerCu);
     hipError_t e;
     if (down) {
         a.n_tiles_n = (w.out + gemm::kTN - 1) / gemm::kTN;
-        if ((e = dispatch_kind(w, SetLds<gemm::DOWN>{})) != hipSuccess) return e;
-        e = dispatch_kind(w, gemm::Launch<gemm::DOWN>{p, s, a, blocks});
+        if (!affine && (e = dispatch_kind(w, SetLds<gemm::DOWN>{})) != hipSuccess) return e;
+        e = dispatch_kind(w, gemm::Launch<gemm::DOWN>{p, s, a, blocks, affine, affine_blocks});
     } else {
         a.n_tiles_n = (w.out + gemm::kTN / 2 - 1) / (gemm::kTN / 2);
-        if ((e = dispatch_kind(w, SetLds<gemm::GATEUP>{})) != hipSuccess) return e;
-        e = dispatch_kind(w, gemm::Launch<gemm::GATEUP>{p, s, a, blocks});
+        if (!affine && (e = dispatch_kind(w, SetLds<gemm::GATEUP>{})) != hipSuccess) return e;
+        e = dispatch_kind(w, gemm::Launch<gemm::GATEUP>{p, s, a, blocks, affine, affine_blocks});
     }
     return e;
 }
@@ -508,7 +764,7 @@ hipError_t launch_gemm_router(Prof *p, hipStream_t s, const WDesc &r, const uint
     a.n_tiles_n = (r.out + gemm::kTN - 1) / gemm::kTN;
     hipError_t e;
     if ((e = dispatch_kind(r, SetLds<gemm::ROUTER>{})) != hipSuccess) return e;
-    return dispatch_kind(r, gemm::Launch<gemm::ROUTER>{p, s, a, gemm_blocks()});
+    return dispatch_kind(r, gemm::Launch<gemm::ROUTER>{p, s, a, gemm_blocks(), false, 0});
 }
 
 }  // namespace moehip

@@ -234,8 +234,8 @@ moe_status run_mfma(moe_gpu *g, const moe_block_weights *w, const Dims &d, const
         TRY(launch_route(p, s, logits, E, K, w->normalize ? 1 : 0, (uint32_t)T, ids, wts));
     }
     TRY(launch_dispatch(p, s, ids, (uint32_t)(T * K), E, counts, offsets, perm, pos));
-    TRY(launch_mfma_experts(p, s, wdesc(w->gate), wdesc(w->up), wdesc(w->down), xb16, offsets, perm,
-                            K, tiles, ntiles, act16, y16));
+    TRY(launch_mfma_experts(p, s, wdesc(w->gate), wdesc(w->up), wdesc(w->down), xb16, (uint32_t)T,
+                            offsets, perm, K, tiles, ntiles, act16, y16));
     const float *so = nullptr, *sgv = nullptr;
     if (w->has_shared) {
         float *sg = ws + L.sh_act, *su = ws + L.sh_up, *sout = ws + L.sh_out, *sgt = ws + L.sh_gate;

@@ -131,20 +131,21 @@ hipError_t launch_grouped_down(Prof *p, hipStream_t s, const WDesc &down, const 
 hipError_t launch_to_bf16(Prof *p, hipStream_t s, const float *x, const float *norm_w, float eps,
                           uint32_t tokens, uint32_t h, uint16_t *y, float *xn);
 hipError_t launch_mfma_experts(Prof *p, hipStream_t s, const WDesc &gate, const WDesc &up,
-                               const WDesc &down, const uint16_t *xb16, const uint32_t *offsets,
-                               const uint32_t *perm, uint32_t k, uint32_t *tiles,
-                               uint32_t *ntiles, uint16_t *act16, uint16_t *y16);
+                               const WDesc &down, const uint16_t *xb16, uint32_t tokens,
+                               const uint32_t *offsets, const uint32_t *perm, uint32_t k,
+                               uint32_t *tiles, uint32_t *ntiles, uint16_t *act16, uint16_t *y16);
 // Grouped expert GEMM over the dispatched segments (k_gemm.hip): down = 0 for
 // gate/up + SwiGLU (w = gate, w2 = up, a_rows = xb16, out = act16), 1 for the
 // down product (w = w2 = down, a_rows = act16, out = y16; the combine applies
-// the routing weights).  tiles/ntiles: M-tiles of gemm_tile_rows() pairs from
+// the routing weights).  a_rows_n: rows of a_rows (tokens, or pairs for the
+// down product).  tiles/ntiles: M-tiles of gemm_tile_rows() pairs from
 // tile_schedule.
 bool gemm_supported(const WDesc &w);
 uint32_t gemm_tile_rows();  // pairs per work item (the M-tiles tile_schedule emits)
 hipError_t launch_grouped_gemm(Prof *p, hipStream_t s, int down, const WDesc &w, const WDesc &w2,
-                               const uint16_t *a_rows, const uint32_t *perm, const uint32_t *offsets,
-                               const uint32_t *tiles, const uint32_t *ntiles, uint32_t k,
-                               uint16_t *out);
+                               const uint16_t *a_rows, uint64_t a_rows_n, const uint32_t *perm,
+                               const uint32_t *offsets, const uint32_t *tiles, const uint32_t *ntiles,
+                               uint32_t k, uint16_t *out);
 hipError_t launch_combine16(Prof *p, hipStream_t s, const uint16_t *y16, const uint32_t *pos,
                             const float *wts, uint32_t k, const float *sh_out, const float *sh_gate,
                             const float *resid, float *out, uint32_t tokens, uint32_t h);

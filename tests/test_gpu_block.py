@@ -10,9 +10,10 @@ import numpy as np
 import pytest
 
 import oracle
-from helpers import (close, config1, config2, config3, config4, config5, hot_bias, rel_max_err,
-                     zipf_bias)
-from hip_backend import PATH_AUTO, PATH_GROUPED, PATH_MFMA, PATH_OPS, BlockWeights, Tensor, synth
+from helpers import (DENSE, HostBlock, close, config1, config2, config3, config4, config5, hot_bias,
+                     rel_max_err, zipf_bias)
+from hip_backend import (BF16, F16, F32, PATH_AUTO, PATH_GROUPED, PATH_MFMA, PATH_OPS, BlockWeights,
+                         Tensor, synth)
 
 pytestmark = pytest.mark.gpu
 
@@ -318,6 +319,27 @@ def test_config4_prefill_sizes(gpu, c4, T):
     err = check_against_oracle(blk, x, got, tokens=sample, bias=bias, tol=BF16_TOL,
                                logit_tol=BF16_TOL)
     print(f"[case] config4 T={T} rel err {err:.3e}", flush=True)
+
+
+@pytest.mark.parametrize("bits,group,st", [(2, 32, BF16), (2, 128, F32), (4, 32, F16), (4, 128, F32),
+                                           (8, 32, F32), (8, 64, F16), (8, 128, BF16)])
+def test_mfma_experts_all_affine_layouts(gpu, bits, group, st):
+    """bf16-MFMA expert products over every code width and scale type (h 256,
+    8 experts, top 2, ff 128, 300 tokens).  The skewed routing gives M-tiles
+    (128 pairs) with one, two, three and four live 32-row slices."""
+    print(f"[case] MFMA experts bits={bits} group={group} st={st}", flush=True)
+    blk = HostBlock(256, 8, 2, 128, 0, {"router": DENSE, "experts": (bits, group, st)},
+                    seed=60 + bits, random_experts=True)
+    bw = blk.upload(gpu)
+    T = 300
+    x = synth.normal(4400 + bits, T * 256).reshape(T, 256)
+    bias = zipf_bias(T, 8, seed=0, s=0.5)
+    got = run_block(gpu, bw, x, T, PATH_MFMA, bias=bias)
+    slices = {(min(c - m, 128) + 31) // 32 for c in np.bincount(got[2].ravel(), minlength=8)
+              for m in range(0, int(c), 128)}
+    assert slices >= {1, 2, 3, 4}
+    check_against_oracle(blk, x, got, tokens=range(0, T, 7), bias=bias, tol=BF16_TOL,
+                         logit_tol=BF16_TOL)
 
 
 def test_mfma_path_with_shared_expert(gpu, c2):
