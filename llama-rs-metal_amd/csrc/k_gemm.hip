@@ -431,19 +431,24 @@ constexpr int kRsrcWord3 = 0x00020000;   // gfx9 buffer resource: raw, untyped
 
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, 0xffffffff, kRsrcWord3);
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p, uint32_t bytes = 0xffffffffu) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, bytes, kRsrcWord3);
 }
 // Position of 16-byte chunk c of A-tile row r inside the row: chunks are
 // XOR-permuted so the 32 rows one fragment read touches spread over the banks.
 __device__ __forceinline__ uint32_t a_chunk(uint32_t r, uint32_t c) { return c ^ ((r ^ (r >> 3)) & 7u); }
 
 // One lane's codes (32 consecutive K values) of its kAfNT weight rows for one
-// K step, with the raw bits of their groups' scales and biases.
+// K step, with the raw bits of their groups' scales and biases (F32 scales).
 template <int BITS>
 struct AfStage {
     uint32_t w[kAfNT][BITS];
     uint32_t s[kAfNT], b[kAfNT];
+};
+// 16-bit scales and biases of one lane's rows for two K steps: the 8 bytes
+// from the (even) group holding the pair's first element.
+struct AfScales {
+    uint32_t s[kAfNT][2], b[kAfNT][2];
 };
 
 // The 8 codes k = 8j .. 8j + 7 of a lane's 32, as floats.
@@ -466,8 +471,10 @@ __device__ __forceinline__ void codes8(const uint32_t *w, int j, float *c) {
 // are neither loaded nor multiplied).  Wave wv owns weight rows
 // [64 wv, 64 wv + 64) of the N-tile (GATEUP: 32 gate rows and the 32 up rows
 // of the same outputs); lane half h feeds K values 32h + 8j + [0, 8) at MFMA
-// step j to both operands.
-template <int MODE, int BITS, int T, int NS>
+// step j to both operands.  GS = log2(group size) for 16-bit scales, whose
+// scale and bias loads then cover two K steps; 0 for F32 scales (one load
+// per step).
+template <int MODE, int BITS, int T, int NS, int GS>
 __device__ __forceinline__ void affine_item(const Args &a, uint8_t *abuf, uint32_t nt, uint32_t e,
                                             uint32_t m0, uint32_t seg_end, int lane, int wv) {
     const int h = lane >> 5, l32 = lane & 31;
@@ -496,8 +503,13 @@ __device__ __forceinline__ void affine_item(const Args &a, uint8_t *abuf, uint32
     }
     const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.a_rows);
     const __amdgpu_buffer_rsrc_t rw[kAfNT] = {buffer_rsrc(a.w.data), buffer_rsrc(MODE == GATEUP ? a.w2.data : a.w.data)};
-    const __amdgpu_buffer_rsrc_t rs[kAfNT] = {buffer_rsrc(a.w.scales), buffer_rsrc(MODE == GATEUP ? a.w2.scales : a.w.scales)};
-    const __amdgpu_buffer_rsrc_t rb[kAfNT] = {buffer_rsrc(a.w.biases), buffer_rsrc(MODE == GATEUP ? a.w2.biases : a.w.biases)};
+    // scale / bias arrays with their true sizes: the two-step loads may run
+    // past the last group, and the hardware returns 0 there
+    const uint32_t sb_bytes = (uint32_t)(((uint64_t)a.w.experts * out * in >> a.w.gshift) * (T == 0 ? 4 : 2));
+    const __amdgpu_buffer_rsrc_t rs[kAfNT] = {buffer_rsrc(a.w.scales, sb_bytes),
+                                              buffer_rsrc(MODE == GATEUP ? a.w2.scales : a.w.scales, sb_bytes)};
+    const __amdgpu_buffer_rsrc_t rb[kAfNT] = {buffer_rsrc(a.w.biases, sb_bytes),
+                                              buffer_rsrc(MODE == GATEUP ? a.w2.biases : a.w.biases, sb_bytes)};
     const uint32_t gshift = a.w.gshift;
 
     f32x16 acc[NS][kAfNT];
@@ -533,22 +545,51 @@ __device__ __forceinline__ void affine_item(const Args &a, uint8_t *abuf, uint32
                     st.w[t][4 * i + 3] = v[3];
                 }
             }
-            const uint32_t g = (el0[t] + kb * kTK) >> gshift;  // 32 codes lie in one group
-            if constexpr (T == 0) {
+            if constexpr (GS == 0) {
+                const uint32_t g = (el0[t] + kb * kTK) >> gshift;  // 32 codes lie in one group
                 st.s[t] = __builtin_amdgcn_raw_buffer_load_b32(rs[t], g * 4, 0, 0);
                 st.b[t] = __builtin_amdgcn_raw_buffer_load_b32(rb[t], g * 4, 0, 0);
-            } else {
-                st.s[t] = __builtin_amdgcn_raw_buffer_load_b16(rs[t], g * 2, 0, 0);
-                st.b[t] = __builtin_amdgcn_raw_buffer_load_b16(rb[t], g * 2, 0, 0);
             }
         }
     };
-    auto compute = [&](const uint8_t *cur, const AfStage<BITS> &sc) {
+    // Two-step scales (kb even): 8 bytes from group (row start + 64 kb) >> GS
+    // rounded down to even, so the load is 4-byte aligned (for GS 5 and 6 the
+    // group is already even: in % 128 == 0).  Within them lane half h finds
+    // step kb + s's group at element (64 s + 32 h) >> GS for GS 5 and 6; for
+    // GS 7 one group spans the two steps, at element (row start + 64 kb) >> 7
+    // mod 2.
+    auto load_sb = [&](AfScales &sc2, uint32_t kb) {
+        if constexpr (GS != 0) {
+#pragma unroll
+            for (int t = 0; t < kAfNT; t++) {
+                const uint32_t g = ((el0[t] - 32 * h + kb * kTK) >> GS) & ~1u;
+                const u32x2 vs = __builtin_amdgcn_raw_buffer_load_b64(rs[t], g * 2, 0, 0);
+                const u32x2 vb = __builtin_amdgcn_raw_buffer_load_b64(rb[t], g * 2, 0, 0);
+                sc2.s[t][0] = vs[0];
+                sc2.s[t][1] = vs[1];
+                sc2.b[t][0] = vb[0];
+                sc2.b[t][1] = vb[1];
+            }
+        }
+    };
+    // raw 16-bit value (in the low half) of step kb + s of weight tile t from
+    // a two-step load
+    auto pick = [&](const uint32_t *pair, int t, int s, uint32_t kb) -> uint32_t {
+        if constexpr (GS == 5) return pair[s] >> (16 * h);
+        else if constexpr (GS == 6) return pair[0] >> (16 * s);
+        else return pair[0] >> (16 * (((el0[t] - 32 * h + kb * kTK) >> 7) & 1));
+    };
+    auto compute = [&](const uint8_t *cur, const AfStage<BITS> &sc, const AfScales &sc2, int s2, uint32_t kb) {
         float sf[kAfNT], bf[kAfNT];
 #pragma unroll
         for (int t = 0; t < kAfNT; t++) {
-            sf[t] = BStage<BITS, T>::scalar(sc.s[t]);
-            bf[t] = BStage<BITS, T>::scalar(sc.b[t]);
+            if constexpr (GS == 0) {
+                sf[t] = BStage<BITS, T>::scalar(sc.s[t]);
+                bf[t] = BStage<BITS, T>::scalar(sc.b[t]);
+            } else {
+                sf[t] = BStage<BITS, T>::scalar(pick(sc2.s[t], t, s2, kb) & 0xffffu);
+                bf[t] = BStage<BITS, T>::scalar(pick(sc2.b[t], t, s2, kb) & 0xffffu);
+            }
         }
 #pragma unroll
         for (int j = 0; j < kTK / 16; j++) {
@@ -581,21 +622,29 @@ __device__ __forceinline__ void affine_item(const Args &a, uint8_t *abuf, uint32
     // DMA for kb + 1 then refills.  Past the last step the loads repeat step
     // nk - 1 into the idle stage.
     AfStage<BITS> bs0, bs1;
+    AfScales sb;
     __builtin_amdgcn_s_waitcnt(0);  // the previous item's last DMA landed
     __builtin_amdgcn_s_barrier();   // and both waves finished reading both stages
     dma(0, 0);
     load_b(bs0, 0);
-    auto step = [&](uint32_t kb, const AfStage<BITS> &sc, AfStage<BITS> &sn) {
+    load_sb(sb, 0);
+    // even step: its scales are element s = 0 of the pair loaded one step
+    // earlier; odd step: element 1, and the next pair is loaded (the compiler
+    // keeps the old pair live until the odd step's compute has read it)
+    for (uint32_t kb = 0; kb < nk; kb += 2) {  // nk is even (in % 128 == 0)
         __builtin_amdgcn_s_waitcnt(0);
         __builtin_amdgcn_s_barrier();
-        const uint32_t kn = min(kb + 1, nk - 1);
-        dma((kb + 1) & 1, kn);
-        load_b(sn, kn);
-        compute(abuf + (kb & 1) * kAfATile, sc);
-    };
-    for (uint32_t kb = 0; kb < nk; kb += 2) {  // nk is even (in % 128 == 0)
-        step(kb, bs0, bs1);
-        step(kb + 1, bs1, bs0);
+        dma(1, kb + 1);
+        load_b(bs1, kb + 1);
+        compute(abuf, bs0, sb, 0, kb);
+        const AfScales cur = sb;
+        __builtin_amdgcn_s_waitcnt(0);
+        __builtin_amdgcn_s_barrier();
+        const uint32_t kn = min(kb + 2, nk - 1);
+        dma(0, kn);
+        load_b(bs0, kn);
+        load_sb(sb, min(kb + 2, nk - 2));
+        compute(abuf + kAfATile, bs1, cur, 1, kb);
     }
     // acc[s][t][r] = C[32 s + 8 (r / 4) + 4 h + r % 4][this wave's column 32 t + l32]
 #pragma unroll
@@ -624,6 +673,16 @@ __device__ __forceinline__ void affine_item(const Args &a, uint8_t *abuf, uint32
     }
 }
 
+template <int MODE, int BITS, int T, int GS>
+__device__ __forceinline__ void affine_live(const Args &a, uint8_t *abuf, uint32_t nt, uint32_t e,
+                                            uint32_t m0, uint32_t seg_end, uint32_t live, int lane,
+                                            int wv) {
+    if (live > 96) affine_item<MODE, BITS, T, 4, GS>(a, abuf, nt, e, m0, seg_end, lane, wv);
+    else if (live > 64) affine_item<MODE, BITS, T, 3, GS>(a, abuf, nt, e, m0, seg_end, lane, wv);
+    else if (live > 32) affine_item<MODE, BITS, T, 2, GS>(a, abuf, nt, e, m0, seg_end, lane, wv);
+    else affine_item<MODE, BITS, T, 1, GS>(a, abuf, nt, e, m0, seg_end, lane, wv);
+}
+
 // Affine GATEUP / DOWN products: same persistent XCD-range schedule as
 // grouped_gemm_kernel, two waves per block, at most 256 VGPRs per lane so two
 // waves share a SIMD.
@@ -643,10 +702,13 @@ void affine_gemm_kernel(Args a) {
         const uint32_t e = a.tiles[2 * mt], m0 = a.tiles[2 * mt + 1];
         const uint32_t seg_end = a.offsets[e + 1];
         const uint32_t live = min(seg_end - m0, (uint32_t)kTM);
-        if (live > 96) affine_item<MODE, BITS, T, 4>(a, abuf, nt, e, m0, seg_end, lane, wv);
-        else if (live > 64) affine_item<MODE, BITS, T, 3>(a, abuf, nt, e, m0, seg_end, lane, wv);
-        else if (live > 32) affine_item<MODE, BITS, T, 2>(a, abuf, nt, e, m0, seg_end, lane, wv);
-        else affine_item<MODE, BITS, T, 1>(a, abuf, nt, e, m0, seg_end, lane, wv);
+        if constexpr (T == 0) {
+            affine_live<MODE, BITS, T, 0>(a, abuf, nt, e, m0, seg_end, live, lane, wv);
+        } else {
+            if (a.w.gshift == 5) affine_live<MODE, BITS, T, 5>(a, abuf, nt, e, m0, seg_end, live, lane, wv);
+            else if (a.w.gshift == 6) affine_live<MODE, BITS, T, 6>(a, abuf, nt, e, m0, seg_end, live, lane, wv);
+            else affine_live<MODE, BITS, T, 7>(a, abuf, nt, e, m0, seg_end, live, lane, wv);
+        }
     }
 }
 
