@@ -13,7 +13,10 @@ step, every step on a fresh N(0,1) token.  Steps are captured into a HIP graph
 of 64 steps and replayed; the timed region is bracketed by stream
 synchronisation (hipEvents on the library's stream measure it).
 
-A third leg runs config 5: the 48-layer MoE-only stack (RMSNorm, MoE block,
+Further legs: config 4 prefill (4096 tokens on the bf16 MFMA path; skip with
+--no-prefill); config 3, the same layers with 8-bit g64 routers and shared
+experts and hot-set routing, at 1, 8, 32 and 64 concurrent tokens (skip with
+--no-batched); config 5, the 48-layer MoE-only stack (RMSNorm, MoE block,
 residual) at the config-2 shapes with 2-bit g32 and 8-bit g128 experts, 256
 decode steps each (skip with --no-stack).
 
@@ -140,6 +143,80 @@ def bench_prefill(gpu, iters=10):
         "segment_max": int(counts.max()), "segment_min": int(counts.min()),
         "kernels_us": k_us,
     }
+
+
+# ---- config 3: 8-bit g64 router and shared expert, decode at 1/8/32/64 tokens ----
+C3_BATCHES = (1, 8, 32, 64)
+C3_CHUNK, C3_REPS = 16, 8  # steps per captured graph, graph replays timed
+MAT8_BYTES = FF * H + 2 * (FF * H // GROUP) * 2  # 8-bit g64 matrix with bf16 scales and biases
+
+
+def hot_bias(tokens, seed, frac=0.2, hot=16, boost=8.0):
+    """Config-3 skew: a seeded `frac` of the tokens gets +boost on `hot` experts."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    hot_ids = rng.choice(E, hot, replace=False)
+    sel = rng.random(tokens) < frac
+    b = np.zeros((tokens, E), np.float32)
+    b[np.ix_(sel, hot_ids)] = boost
+    return b
+
+
+def c3_layers(gpu, layers):
+    """Config-3 layers over the resident config-2 routed experts: 8-bit g64
+    routers and shared experts (quantised from N(0, 0.02)), one per layer."""
+    out = []
+    for l, bw in enumerate(layers):
+        s = 800 * 100 + 10 * l
+        q8 = lambda seed, dims: Tensor.affine(dims, *synth.quantize_affine(
+            synth.normal(seed, int(np.prod(dims)), 0.0, 0.02), 8, GROUP, BF16), 8, GROUP, BF16)
+        router = gpu.weight_tensor(q8(s, [H, E]))
+        shared = tuple(gpu.weight_tensor(q8(s + 1 + i, d))
+                       for i, d in enumerate(([H, FFS], [H, FFS], [FFS, H])))
+        sgate = gpu.weight_tensor(Tensor.dense([H], synth.normal(s + 5, H, 0.0, 0.02)))
+        _, g, u, d, _, _ = bw.keep
+        out.append(BlockWeights(router, g, u, d, K, True, shared, sgate))
+    return out
+
+
+def bench_batched(gpu, layers, T):
+    """Config 3 at T concurrent tokens: C3_CHUNK steps over the rotated layers
+    (fresh N(0,1) tokens and hot-set biases per step) captured into a graph
+    and replayed.  Bytes per step: the distinct routed experts the step
+    selects (3 matrices each) plus the 8-bit router and shared expert."""
+    xs = gpu.upload(synth.normal(8000 + T, C3_CHUNK * T * H))
+    outs = gpu.zeros(C3_CHUNK * T * H)
+    bias = gpu.upload(np.concatenate([hot_bias(T, 8100 + 31 * T + j) for j in range(C3_CHUNK)]))
+    ids = gpu.zeros(C3_CHUNK * T * K)
+    ws = gpu.zeros(layers[0].workspace_elems(T))
+
+    def issue(b, j, ids_out=None):
+        b.moe_block(layers[j % len(layers)], xs.view(j * T * H, T * H), outs.view(j * T * H, T * H),
+                    T, ws, logit_bias=bias.view(j * T * E, T * E), ids_out=ids_out)
+
+    with gpu.batch() as b:
+        for j in range(C3_CHUNK):
+            issue(b, j, ids.view(j * T * K, T * K))
+    sel = gpu.read_u32(ids).reshape(C3_CHUNK, T * K)
+    distinct = [len(np.unique(r)) for r in sel]
+    step_bytes = [dn * 3 * MAT_BYTES + 4 * MAT8_BYTES + H * 4 for dn in distinct]
+    cap = gpu.capture()
+    with cap as b:
+        for j in range(C3_CHUNK):
+            issue(b, j)
+    with gpu.batch() as b:
+        b.graph(cap.graph)
+    with gpu.batch() as b:
+        for _ in range(C3_REPS):
+            b.graph(cap.graph)
+    per_step = b.seconds / (C3_REPS * C3_CHUNK)
+    for buf in (xs, outs, bias, ids, ws):
+        gpu.release(buf)
+    gbps = np.mean(step_bytes) / per_step / 1e9
+    return {"tokens": T, "path": "fused decode" if T == 1 else "grouped (VALU)",
+            "us_per_step": round(per_step * 1e6, 3), "tokens_per_s": round(T / per_step, 1),
+            "distinct_experts_per_step": round(float(np.mean(distinct)), 1),
+            "bytes_per_step": int(np.mean(step_bytes)),
+            "achieved_GBps": round(gbps, 1), "hbm_frac": round(gbps * 1e9 / HBM_PEAK, 4)}
 
 
 # ---- config 5: 48-layer MoE-only stack (RMSNorm, MoE block, residual) ----
@@ -277,6 +354,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-stack", action="store_true")
+    ap.add_argument("--no-batched", action="store_true")
     ap.add_argument("--traffic-probe", choices=["decode", "prefill"], default=None,
                     help="short eager workload for rocprofv3 --pmc runs (no timing output)")
     args = ap.parse_args()
@@ -397,6 +475,15 @@ def main():
         result["prefill"] = bench_prefill(gpu)
         log(f"[bench] prefill: {result['prefill']['ms_per_layer']} ms/layer, "
             f"{result['prefill']['achieved_TFLOPs']} TFLOP/s")
+    if not args.no_batched:
+        c3 = c3_layers(gpu, layers)
+        result["batched"] = []
+        for T in C3_BATCHES:
+            r = bench_batched(gpu, c3, T)
+            log(f"[bench] config-3 T={T}: {r['us_per_step']} us/step, {r['tokens_per_s']} tokens/s, "
+                f"{r['achieved_GBps']} GB/s over {r['distinct_experts_per_step']} experts")
+            result["batched"].append(r)
+        del c3
     if not args.no_stack:
         result["stack"] = []
         for v in STACK_VARIANTS:

@@ -196,7 +196,9 @@ typedef struct {
 /* Path selection for moe_block. */
 enum {
     MOE_PATH_AUTO = 0,   /* fused decode for one token; bf16 MFMA when the mean expert
-                            segment holds >= 16 pairs; VALU grouped otherwise */
+                            segment holds >= 16 pairs; otherwise the batched decode
+                            (weight rows streamed once per run of 8 inputs) where the
+                            shapes allow it, else VALU grouped */
     MOE_PATH_OPS = 1,     /* the reference's per-token op sequence (execute.rs:208-233) */
     MOE_PATH_GROUPED = 2, /* dispatch + grouped expert products on VALU (F32) */
     MOE_PATH_MFMA = 3     /* dispatch + grouped expert products on bf16 MFMA */

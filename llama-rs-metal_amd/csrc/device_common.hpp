@@ -141,10 +141,17 @@ __device__ __forceinline__ float funkey(uint32_t k) {
 // Max over the wave of non-NaN floats (NaN inputs must be pre-filtered).
 __device__ __forceinline__ float wave_max(float v) { return funkey(wave_max_u32(fkey(v))); }
 
-// Byte N of a word as float (selects to v_cvt_f32_ubyteN).
+// Byte N of a word as float: one v_cvt_f32_ubyteN (written out because the
+// compiler otherwise emits a bit-field extract plus v_cvt_f32_ubyte0 for
+// bytes 1-3).
 template <int N>
 __device__ __forceinline__ float ubyte_f32(uint32_t v) {
-    return (float)((v >> (8 * N)) & 0xffu);
+    float r;
+    if constexpr (N == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
+    else if constexpr (N == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
+    else if constexpr (N == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
+    else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
+    return r;
 }
 
 // Codes of one packed word as floats, low bits first (affine.metal:17-19,

@@ -167,6 +167,12 @@ hipError_t launch_to_bf16(Prof *p, hipStream_t s, const float *x, const float *n
                          h, y, xn);
 }
 
+hipError_t launch_tile_schedule(Prof *p, hipStream_t s, const uint32_t *offsets, uint32_t experts,
+                                uint32_t tm, uint32_t *tiles, uint32_t *ntiles) {
+    return launch_kernel(p, "tile_schedule", tile_schedule_kernel, dim3(1), dim3(64), 0, s, offsets,
+                         experts, tm, tiles, ntiles);
+}
+
 hipError_t launch_mfma_experts(Prof *p, hipStream_t s, const WDesc &gate, const WDesc &up,
                                const WDesc &down, const uint16_t *xb16, uint32_t tokens,
                                const uint32_t *offsets, const uint32_t *perm, uint32_t k,

@@ -5,10 +5,14 @@
 //   MOE_PATH_OPS      the reference's own per-token op sequence (14 ops per token)
 //   MOE_PATH_GROUPED  token-batched: route all tokens, dispatch by expert,
 //                     grouped expert products, one combine
-//   MOE_PATH_AUTO     fused 3-kernel decode for one token, grouped otherwise
+//   MOE_PATH_AUTO     fused 3-kernel decode for one token; bf16 MFMA for
+//                     prefill-sized segments; the batched decode
+//                     (k_batched.hip) for a few tokens; grouped otherwise
 #include "abi_common.hpp"
 
 namespace {
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 struct WsLayout {
     uint64_t logits, ids, weights, counts, offsets, perm, pos, act, yexp, sh_act, sh_up, sh_gate,
@@ -47,7 +51,7 @@ WsLayout ws_layout(uint64_t T, uint64_t E, uint64_t K, uint64_t h, uint64_t ff, 
     take(L.xb16, (T * h + 1) / 2);
     take(L.act16, (T * K * ff + 1) / 2);
     take(L.y16, (T * K * h + 1) / 2);
-    take(L.tiles, 2 * ((T * K + 127) / 128 + E + 1));
+    take(L.tiles, 2 * ((T * K + 7) / 8 + E + 1));  // MFMA tiles of 128 pairs, batched runs of 8
     take(L.ntiles, 1);
     L.total = o;
     return L;
@@ -185,6 +189,65 @@ moe_status run_grouped(moe_gpu *g, const moe_block_weights *w, const Dims &d, co
     }
     TRY(launch_combine(p, s, yexp, pos, wts, K, so, sgv, io->residual ? xres : nullptr, out,
                        (uint32_t)T, (uint32_t)d.h));
+    return MOE_OK;
+}
+
+// Batched decode (k_batched.hip): several tokens whose expert segments are
+// too short for the MFMA path.  Same composition as run_grouped; every
+// product streams its weight rows once per run of seg_tokens() inputs.
+bool batched_ok(const moe_block_weights *w) {
+    const WDesc G = wdesc(w->gate), U = wdesc(w->up), D = wdesc(w->down);
+    if (!seg_supported(wdesc(w->router)) || !seg_supported(G) || !seg_supported(U) ||
+        !seg_supported(D) || G.bits != U.bits || G.type != U.type)
+        return false;
+    if (w->has_shared) {
+        const WDesc SG = wdesc(w->shared_gate), SU = wdesc(w->shared_up);
+        if (!seg_supported(SG) || !seg_supported(SU) || !seg_supported(wdesc(w->shared_down)) ||
+            !seg_supported(gate_inp_desc(w->shared_gate_inp)) || SG.bits != SU.bits ||
+            SG.type != SU.type)
+            return false;
+    }
+    return true;
+}
+
+moe_status run_batched(moe_gpu *g, const moe_block_weights *w, const Dims &d, const float *xin,
+                       const float *xres, float *out, uint64_t T, const moe_block_io *io,
+                       const WsLayout &L, float *ws, float *logits, uint32_t *ids, float *wts) {
+    Prof *p = &g->prof;
+    hipStream_t s = g->stream;
+    const uint32_t K = (uint32_t)d.K, E = (uint32_t)d.E, t32 = (uint32_t)T;
+    uint32_t *counts = reinterpret_cast<uint32_t *>(ws + L.counts);
+    uint32_t *offsets = reinterpret_cast<uint32_t *>(ws + L.offsets);
+    uint32_t *perm = reinterpret_cast<uint32_t *>(ws + L.perm);
+    uint32_t *pos = reinterpret_cast<uint32_t *>(ws + L.pos);
+    uint32_t *tiles = reinterpret_cast<uint32_t *>(ws + L.tiles);
+    uint32_t *ntiles = reinterpret_cast<uint32_t *>(ws + L.ntiles);
+    float *act = ws + L.act, *yexp = ws + L.yexp;
+    const uint32_t runs = seg_max_entries(t32, 0), entries = seg_max_entries(t32 * K, E);
+    const float *bias = has(io->logit_bias) ? fp(io->logit_bias) : nullptr;
+    TRY(launch_seg_rows(p, s, "seg_router", wdesc(w->router), xin, nullptr, nullptr, nullptr, t32, runs,
+                        bias, logits));
+    TRY(launch_route(p, s, logits, E, K, w->normalize ? 1 : 0, t32, ids, wts));
+    TRY(launch_dispatch(p, s, ids, t32 * K, E, counts, offsets, perm, pos));
+    TRY(launch_tile_schedule(p, s, offsets, E, seg_tokens(), tiles, ntiles));
+    TRY(launch_seg_gateup(p, s, "seg_gateup", wdesc(w->gate), wdesc(w->up), xin, perm, K, tiles, ntiles,
+                          offsets, 0, entries, act));
+    TRY(launch_seg_rows(p, s, "seg_down", wdesc(w->down), act, tiles, ntiles, offsets, 0, entries,
+                        nullptr, yexp));
+    const float *so = nullptr, *sgv = nullptr;
+    if (w->has_shared) {
+        float *sh = ws + L.sh_act, *sout = ws + L.sh_out, *sgt = ws + L.sh_gate;
+        TRY(launch_seg_gateup(p, s, "seg_shared_gateup", wdesc(w->shared_gate), wdesc(w->shared_up), xin,
+                              nullptr, 1, nullptr, nullptr, nullptr, t32, runs, sh));
+        TRY(launch_seg_rows(p, s, "seg_shared_down", wdesc(w->shared_down), sh, nullptr, nullptr, nullptr,
+                            t32, runs, nullptr, sout));
+        TRY(launch_seg_rows(p, s, "seg_shared_gate", gate_inp_desc(w->shared_gate_inp), xin, nullptr,
+                            nullptr, nullptr, t32, runs, nullptr, sgt));
+        so = sout;
+        sgv = sgt;
+    }
+    TRY(launch_combine(p, s, yexp, pos, wts, K, so, sgv, io->residual ? xres : nullptr, out, t32,
+                       (uint32_t)d.h));
     return MOE_OK;
 }
 
@@ -369,6 +432,8 @@ moe_status moe_block(moe_gpu *g, const moe_block_weights *w, moe_buffer x, moe_b
     }
     if (io->path == MOE_PATH_OPS)
         return run_ops(g, w, d, xin, xraw, o, T, io, L, ws, logits, ids, wts);
+    if (io->path == MOE_PATH_AUTO && batched_ok(w) && aligned16(xin) && aligned16(ws))
+        return run_batched(g, w, d, xin, xraw, o, T, io, L, ws, logits, ids, wts);
     return run_grouped(g, w, d, xin, xraw, o, T, io, L, ws, logits, ids, wts);
 }
 

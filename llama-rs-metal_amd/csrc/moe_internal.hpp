@@ -150,6 +150,27 @@ hipError_t launch_combine16(Prof *p, hipStream_t s, const uint16_t *y16, const u
                             const float *wts, uint32_t k, const float *sh_out, const float *sh_gate,
                             const float *resid, float *out, uint32_t tokens, uint32_t h);
 
+// ---- batched decode (k_batched.hip) ----
+// Row products over work entries of at most seg_tokens() input rows: entries
+// from tile_schedule over the dispatch's segments (tiles, ntiles, offsets),
+// or, with tiles == nullptr, runs over the n input rows of one weight.
+// `entries` bounds the grid (seg_max_entries); surplus entries exit.
+bool seg_supported(const WDesc &w);  // whole 32-element chunks, in / 32 a power of two <= 64
+uint32_t seg_tokens();
+uint32_t seg_max_entries(uint32_t pairs, uint32_t experts);  // experts 0: runs over `pairs` rows
+hipError_t launch_seg_gateup(Prof *p, hipStream_t s, const char *name, const WDesc &gate,
+                             const WDesc &up, const float *x, const uint32_t *perm, uint32_t k,
+                             const uint32_t *tiles, const uint32_t *ntiles, const uint32_t *offsets,
+                             uint32_t n, uint32_t entries, float *act);
+hipError_t launch_seg_rows(Prof *p, hipStream_t s, const char *name, const WDesc &w,
+                           const float *in, const uint32_t *tiles, const uint32_t *ntiles,
+                           const uint32_t *offsets, uint32_t n, uint32_t entries, const float *bias,
+                           float *out);
+// (expert, first position) of every run of `tm` pairs of the non-empty
+// segments, and their count (k_mfma.hip)
+hipError_t launch_tile_schedule(Prof *p, hipStream_t s, const uint32_t *offsets, uint32_t experts,
+                                uint32_t tm, uint32_t *tiles, uint32_t *ntiles);
+
 // ---- fused single-token decode (k_decode.hip) ----
 struct DecodeArgs {
     WDesc router, gate, up, down, sg, su, sd, sgi;
