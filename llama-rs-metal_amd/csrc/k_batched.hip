@@ -17,14 +17,16 @@
 //
 // Entries: either the dispatch's segments cut into runs of kSegTokens pairs
 // (tile_schedule: (expert, first pair); the run ends at the segment end), or
-// runs of kSegTokens rows over [0, n) of a single weight.
+// runs of kSegRun rows over [0, n) of a single weight.
 #include "lanerows.hpp"
 #include "rowdot.hpp"
 
 namespace moehip {
 
-constexpr uint32_t kSegTokens = 8;  // input rows per work entry
-constexpr int kSegGateItems = 1;    // kGateFR-row items of gate (and of up) rows per wave
+constexpr uint32_t kSegTokens = 8;  // pairs per work entry over the dispatched segments
+constexpr uint32_t kSegRun = 2;     // input rows per entry over all tokens (router, shared
+                                    // expert): small weights, so more waves beat re-reads
+constexpr int kSegGateItems = 2;    // kGateFR-row items of gate (and of up) rows per wave
 constexpr int kSegRowsFR = 4;       // row instructions per wave in seg_rows
 
 struct SegArgs {
@@ -50,9 +52,9 @@ __device__ __forceinline__ bool seg_entry(const SegArgs &a, uint32_t i, uint32_t
         end = min(a.offsets[e + 1], beg + kSegTokens);
     } else {
         e = 0;
-        beg = i * kSegTokens;
+        beg = i * kSegRun;
         if (beg >= a.n) return false;
-        end = min(a.n, beg + kSegTokens);
+        end = min(a.n, beg + kSegRun);
     }
     return true;
 }
@@ -192,9 +194,9 @@ static bool chunk_rows_ok(const WDesc &w) {
 
 bool seg_supported(const WDesc &w) { return chunk_rows_ok(w); }
 
-static uint32_t seg_entries(uint32_t n) { return (n + kSegTokens - 1) / kSegTokens; }
 uint32_t seg_max_entries(uint32_t pairs, uint32_t experts) {
-    return seg_entries(pairs) + (experts < pairs ? experts : pairs);
+    if (experts == 0) return (pairs + kSegRun - 1) / kSegRun;
+    return (pairs + kSegTokens - 1) / kSegTokens + (experts < pairs ? experts : pairs);
 }
 uint32_t seg_tokens() { return kSegTokens; }
 
