@@ -212,7 +212,7 @@ def bench_batched(gpu, layers, T):
     for buf in (xs, outs, bias, ids, ws):
         gpu.release(buf)
     gbps = np.mean(step_bytes) / per_step / 1e9
-    return {"tokens": T, "path": "fused decode" if T == 1 else "grouped (VALU)",
+    return {"tokens": T, "path": "fused decode" if T == 1 else "batched decode",
             "us_per_step": round(per_step * 1e6, 3), "tokens_per_s": round(T / per_step, 1),
             "distinct_experts_per_step": round(float(np.mean(distinct)), 1),
             "bytes_per_step": int(np.mean(step_bytes)),

@@ -190,6 +190,36 @@ def test_config3_mixed_precision_hot_set(gpu, c3, T):
     check_against_oracle(blk, x, got, tokens=sample, bias=bias)
 
 
+@pytest.mark.parametrize("experts", [DENSE, (2, 32, BF16), (2, 128, F32), (4, 32, F16),
+                                     (8, 64, F16), (8, 128, BF16)])
+@pytest.mark.parametrize("T", [2, 5, 9])
+def test_batched_decode_layouts(gpu, experts, T):
+    """The batched decode kernels (AUTO with T >= 2 and short expert
+    segments) over every code width and scale type, on rows whose chunk counts
+    take the run-time lanes-per-row form (h 256, ff 128, shared ff 64) and a
+    router of 24 rows (not a multiple of a wave's rows).  Every token gets a
+    boost on two experts, so at T = 9 their segments span two 8-pair entries;
+    odd T leaves a one-row run over the all-token products."""
+    print(f"[case] batched experts={experts} T={T}", flush=True)
+    kinds = {"router": DENSE if experts == DENSE else (8, 64, BF16), "experts": experts,
+             "shared": DENSE if experts == DENSE else (8, 32, BF16), "shared_gate": DENSE}
+    blk = HostBlock(256, 24, 4, 128, 64, kinds, seed=70 + T, random_experts=experts != DENSE)
+    bw = blk.upload(gpu)
+    x = synth.normal(4600 + T, T * 256).reshape(T, 256)
+    bias = hot_bias(T, 24, seed=T, frac=1.0, hot=2, boost=8.0)
+    gpu.profile_reset()
+    gpu.profile(True)
+    got = run_block(gpu, bw, x, T, PATH_AUTO, bias=bias)
+    prof = gpu.profile_read()
+    gpu.profile(False)
+    for k in ("seg_router", "seg_gateup", "seg_down", "seg_shared_gateup", "seg_shared_down"):
+        assert k in prof and prof[k][0] == 1, k
+    check_against_oracle(blk, x, got, bias=bias)
+    ref = run_block(gpu, bw, x, T, PATH_GROUPED, bias=bias)
+    assert np.array_equal(got[2], ref[2])
+    assert rel_max_err(got[0], ref[0]) <= F32_TOL
+
+
 # ------------------------------------------------------------------ config 5 --
 @pytest.fixture(scope="module")
 def c5(gpu):
