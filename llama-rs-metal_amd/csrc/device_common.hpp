@@ -29,6 +29,14 @@ __device__ __forceinline__ float load_scalar(const void *p, uint64_t i) {
     }
 }
 
+// Raw (untyped) buffer resource over `bytes` bytes at p (gfx9 descriptor word
+// 3): loads through it take a scalar base and a 32-bit offset, and return 0
+// past `bytes`.
+constexpr int kRsrcWord3 = 0x00020000;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p, uint32_t bytes = 0xffffffffu) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, bytes, kRsrcWord3);
+}
+
 // Raw bits of one such scalar, converted later by raw_to_f32: lets a caller
 // issue every load before the first conversion waits on one.
 template <int T>

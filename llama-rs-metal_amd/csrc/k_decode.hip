@@ -108,8 +108,10 @@ __device__ __forceinline__ void shared_item(const DecodeKArgs &a, uint32_t item,
 
 // One wave per block.  Waves [0, K*items) route the token (exactly, from the
 // logits) and then compute kGateFR*rpi SwiGLU outputs of one selected expert;
-// the remaining waves compute the shared expert's and need no routing, so
-// their loads overlap the others' routing.
+// the next waves compute the shared expert's and need no routing, so their
+// loads overlap the others' routing; the last wave derives the ids and
+// weights the down kernel reads (the full selection, off the other waves'
+// path).
 template <int BITS, int ST>
 __global__ __launch_bounds__(64) void decode_gateup_kernel(DecodeKArgs a) {
     extern __shared__ float route_vals[];  // E floats (routing with E > 1024 only)
@@ -120,10 +122,20 @@ __global__ __launch_bounds__(64) void decode_gateup_kernel(DecodeKArgs a) {
     const uint32_t lpr = a.lpr_h, rpi = 64u / lpr, sub = lane / lpr, cl = lane % lpr;
     const uint32_t wave_id = blockIdx.x;
     const uint32_t routed_waves = a.k * a.n_gate_waves_per_expert;
+    const uint32_t shared_waves = a.has_shared ? a.n_shared_waves : 0u;
     XChunk X;
-    X.load(a.x, a.norm_w, cl);
+    if (wave_id >= routed_waves + shared_waves) {
+        // route (sampling.metal:1-36): all K ids and weights
+        route_one_wave(&route_lds, route_vals, a.logits, a.E, a.k, (int)a.normalize, s_ids, s_w, lane);
+        __syncthreads();
+        if (lane < a.k) {
+            a.ids[lane] = s_ids[lane];
+            a.weights[lane] = s_w[lane];
+        }
+        return;
+    }
     if (wave_id >= routed_waves) {
-        if (!a.has_shared) return;
+        X.load(a.x, a.norm_w, cl);
         const uint32_t item = wave_id - routed_waves;
         switch (a.sg.bits) {
         case 2: shared_item<2, ST>(a, item, sub, cl, X); break;
@@ -132,23 +144,13 @@ __global__ __launch_bounds__(64) void decode_gateup_kernel(DecodeKArgs a) {
         }
         return;
     }
-    // route (sampling.metal:1-36), exact, redundantly per wave: wave 0 derives
-    // the ids and weights the down kernel reads, every other wave only the id
-    // of its own selection pass kk
+    // the id of this wave's selection pass kk of the same routing; the input
+    // slice loads issue once the logits have arrived (before them, the
+    // logits waited behind them)
     const uint32_t kk = wave_id / a.n_gate_waves_per_expert;
     const uint32_t item = wave_id % a.n_gate_waves_per_expert;
-    uint32_t e;  // < E by construction of route
-    if (wave_id == 0) {
-        route_one_wave(&route_lds, route_vals, a.logits, a.E, a.k, (int)a.normalize, s_ids, s_w, lane);
-        __syncthreads();
-        if (lane < a.k) {
-            a.ids[lane] = s_ids[lane];
-            a.weights[lane] = s_w[lane];
-        }
-        e = s_ids[0];
-    } else {
-        e = route_one_id(&route_lds, route_vals, a.logits, a.E, a.k, kk, lane);
-    }
+    const uint32_t e = route_one_id(&route_lds, route_vals, a.logits, a.E, a.k, kk, lane,
+                                    [&]() { X.load(a.x, a.norm_w, cl); });  // < E by construction
     uint64_t rows[kGateFR];
     bool ok[kGateFR];
 #pragma unroll
@@ -319,7 +321,8 @@ static hipError_t launch_decode_t(Prof *p, hipStream_t s, const DecodeKArgs &k) 
     hipError_t e = launch_kernel(p, "decode_pre", decode_pre_kernel<ST>, dim3(pre_waves), dim3(64), 0,
                                  s, k);
     if (e != hipSuccess) return e;
-    const uint32_t gate_waves = k.k * k.n_gate_waves_per_expert + (k.has_shared ? k.n_shared_waves : 0);
+    // routed waves, shared-expert waves, and the wave that writes ids and weights
+    const uint32_t gate_waves = k.k * k.n_gate_waves_per_expert + (k.has_shared ? k.n_shared_waves : 0) + 1;
     const size_t lds = k.E > 1024 ? (size_t)k.E * sizeof(float) : 0;
     e = launch_kernel(p, "decode_gateup", decode_gateup_kernel<BITS, ST>, dim3(gate_waves), dim3(64),
                       lds, s, k);

@@ -427,13 +427,8 @@ constexpr int kAfThreads = 128;     // two waves
 constexpr int kAfBlocksPerCu = 4;   // 4 x 32 KiB of LDS, 2 waves per SIMD
 constexpr int kAfNT = 2;            // 32-row weight tiles per wave
 constexpr int kAfATile = kTM * kTK * 2;  // one A stage: kTM rows x 128 bytes
-constexpr int kRsrcWord3 = 0x00020000;   // gfx9 buffer resource: raw, untyped
 
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p, uint32_t bytes = 0xffffffffu) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, bytes, kRsrcWord3);
-}
 // Position of 16-byte chunk c of A-tile row r inside the row: chunks are
 // XOR-permuted so the 32 rows one fragment read touches spread over the banks.
 __device__ __forceinline__ uint32_t a_chunk(uint32_t r, uint32_t c) { return c ^ ((r ^ (r >> 3)) & 7u); }

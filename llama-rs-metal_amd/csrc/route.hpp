@@ -296,12 +296,20 @@ __device__ __forceinline__ void route_one_wave(RouteLds *L, float *vals,
 }
 
 // Only the id selected by pass `want` (want < K <= 64) of the same routing;
-// no weights.  Every lane returns it.
-template <int R>
+// no weights.  Every lane returns it.  `after_load` runs once the logits are
+// in registers and before the selection arithmetic: a caller issues its other
+// loads there, so the logits do not wait behind them and they arrive during
+// the selection.
+template <int R, typename F>
 __device__ __forceinline__ uint32_t route_id_regs(RouteLds *L, const float *__restrict__ logits,
-                                                  uint32_t E, uint32_t K, uint32_t want, int lane) {
+                                                  uint32_t E, uint32_t K, uint32_t want, int lane,
+                                                  F &&after_load) {
     float v[R];
     load_logits<R>(logits, E, lane, v);
+#pragma unroll
+    for (int i = 0; i < R; i++) asm volatile("" : "+v"(v[i]));
+    asm volatile("" ::: "memory");
+    after_load();
     uint64_t mine;
     uint32_t r;
     const uint32_t total = rank_candidates<R>(L, v, K, lane, mine, r);
@@ -314,19 +322,21 @@ __device__ __forceinline__ uint32_t route_id_regs(RouteLds *L, const float *__re
     wave_lds_sync();
     return L->sj[want];
 }
+template <typename F>
 __device__ __forceinline__ uint32_t route_one_id(RouteLds *L, float *vals,
                                                  const float *__restrict__ logits, uint32_t E,
-                                                 uint32_t K, uint32_t want, int lane) {
+                                                 uint32_t K, uint32_t want, int lane, F &&after_load) {
     if (E > 1024) {
+        after_load();
         route_wave_lds(vals, logits, E, K, 0, L->sj, L->sv, lane);
         wave_lds_sync();
         return L->sj[want];
     }
-    if (E <= 64) return route_id_regs<1>(L, logits, E, K, want, lane);
-    if (E <= 128) return route_id_regs<2>(L, logits, E, K, want, lane);
-    if (E <= 256) return route_id_regs<4>(L, logits, E, K, want, lane);
-    if (E <= 512) return route_id_regs<8>(L, logits, E, K, want, lane);
-    return route_id_regs<16>(L, logits, E, K, want, lane);
+    if (E <= 64) return route_id_regs<1>(L, logits, E, K, want, lane, after_load);
+    if (E <= 128) return route_id_regs<2>(L, logits, E, K, want, lane, after_load);
+    if (E <= 256) return route_id_regs<4>(L, logits, E, K, want, lane, after_load);
+    if (E <= 512) return route_id_regs<8>(L, logits, E, K, want, lane, after_load);
+    return route_id_regs<16>(L, logits, E, K, want, lane, after_load);
 }
 
 }  // namespace moehip
