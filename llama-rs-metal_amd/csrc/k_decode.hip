@@ -28,24 +28,34 @@ struct DecodeKArgs {
 };
 
 constexpr int kDownFR = 2;    // output rows per sub-wave in decode_down
+constexpr int kPreFR = 2;     // router rows per sub-wave in decode_pre (one input slice each)
 
 // ------------------------------------------------------------------ pre --
-// One wave per block: router rows (and the shared expert's scalar gate row).
+// One wave per block: kPreFR router rows per sub-wave (and the shared
+// expert's scalar gate row).
 template <int BR, int TR>
 __device__ __forceinline__ void router_item(const DecodeKArgs &a, uint32_t wave_id, uint32_t sub,
                                             uint32_t cl, XChunk &X) {
     // router GEMV rows (Batch::matmul(router), crates/model-runtime/src/execute.rs:220)
     const uint32_t lpr = a.lpr_h, rpi = 64u / lpr;
-    const uint64_t e = (uint64_t)wave_id * rpi + sub;
-    const bool ok = e < a.E;
-    LaneRows<BR, TR, 1> L;
-    L.load(a.router, &e, &ok, cl, a.h / 32);
+    uint64_t e[kPreFR];
+    bool ok[kPreFR];
+#pragma unroll
+    for (int f = 0; f < kPreFR; f++) {
+        e[f] = ((uint64_t)wave_id * kPreFR + f) * rpi + sub;
+        ok[f] = e[f] < a.E;
+    }
+    LaneRows<BR, TR, kPreFR> L;
+    L.load(a.router, e, ok, cl, a.h / 32);
     loads_issued();
     const float xsum = X.finish(a.norm_w, a.eps, a.h, (int)lpr);
-    float v;
-    L.dot(X.xr, xsum, &v);
-    v = subwave_sum(v, (int)lpr);
-    if (ok && cl == 0) a.logits[e] = a.logit_bias ? v + a.logit_bias[e] : v;
+    float v[kPreFR];
+    L.dot(X.xr, xsum, v);
+#pragma unroll
+    for (int f = 0; f < kPreFR; f++) {
+        const float r = subwave_sum(v[f], (int)lpr);
+        if (ok[f] && cl == 0) a.logits[e[f]] = a.logit_bias ? r + a.logit_bias[e[f]] : r;
+    }
 }
 
 template <int ST>
@@ -342,7 +352,7 @@ hipError_t launch_decode(Prof *p, hipStream_t s, const DecodeArgs &a) {
     k.h = a.gate.in; k.ff = a.gate.out; k.ffs = a.has_shared ? a.sg.out : 0; k.E = a.router.out;
     k.lpr_h = k.h / 32; k.lpr_f = k.ff / 32;
     const uint32_t rpi_h = 64u / k.lpr_h;
-    k.n_router_waves = (k.E + rpi_h - 1) / rpi_h;
+    k.n_router_waves = (k.E + rpi_h * kPreFR - 1) / (rpi_h * kPreFR);
     k.n_shared_waves = (k.ffs + rpi_h * kGateFR - 1) / (rpi_h * kGateFR);
     k.n_gate_waves_per_expert = (k.ff + rpi_h * kGateFR - 1) / (rpi_h * kGateFR);
     k.x = a.x; k.norm_w = a.norm_w; k.eps = a.eps; k.logit_bias = a.logit_bias; k.resid = a.resid;
