@@ -96,8 +96,10 @@ def zipf_bias(tokens, experts, seed, s=1.1):
     return np.broadcast_to((-s * np.log(rank)).astype(np.float32), (tokens, experts)).copy()
 
 
-def bench_prefill(gpu, iters=10):
-    """Config 4: one MoE layer over 4096 tokens, Zipf(1.1)-skewed routing."""
+def bench_prefill(gpu, iters=10, packed=True):
+    """Config 4: one MoE layer over 4096 tokens, Zipf(1.1)-skewed routing.
+    With `packed`, the expert weights also get their MFMA tile-order copies
+    (moe_pack_weight, made once before timing), which the MFMA path reads."""
     s = 600 * 100
     router = Tensor.affine([P_H, P_E], *synth.random_affine(s + 1, P_H * P_E, 4, 64, BF16), 4, 64,
                            BF16)
@@ -105,7 +107,8 @@ def bench_prefill(gpu, iters=10):
                         BF16)
           for i, d in enumerate(([P_H, P_FF, P_E], [P_H, P_FF, P_E], [P_FF, P_H, P_E]))]
     w = [gpu.weight_tensor(t) for t in [router, *ex]]
-    bw = BlockWeights(w[0], w[1], w[2], w[3], P_K, True)
+    pk = [gpu.pack_weight(t) for t in w[1:]] if packed else None
+    bw = BlockWeights(w[0], w[1], w[2], w[3], P_K, True, packed=pk)
     x = gpu.upload(synth.normal(6060, P_T * P_H))
     out = gpu.zeros(P_T * P_H)
     ws = gpu.zeros(bw.workspace_elems(P_T))
@@ -133,6 +136,7 @@ def bench_prefill(gpu, iters=10):
     return {
         "workload": "config4: Qwen3-30B-A3B MoE layer prefill, 4096 tokens (h2048 E128 top8 "
                     "ff768, 4-bit g64 bf16, Zipf(1.1) router skew), path bf16 MFMA",
+        "expert_weights": "MFMA tile-order copies (moe_pack_weight)" if packed else "row-major",
         "tokens_per_s": round(P_T / t, 1),
         "ms_per_layer": round(t * 1e3, 4),
         "expert_flops": PREFILL_FLOPS,

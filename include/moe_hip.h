@@ -175,6 +175,22 @@ moe_status moe_dispatch(moe_gpu *gpu, moe_buffer ids, uint64_t tokens, uint64_t 
                         uint64_t experts, moe_buffer counts, moe_buffer offsets, moe_buffer perm,
                         moe_buffer pos);
 
+/* A copy of an affine expert weight in MFMA tile order (no reference
+ * counterpart: the Metal kernels read the row-major tensor).  The bf16 MFMA
+ * prefill path wants one weight row per lane pair, so from the row-major
+ * tensor each of its code loads reads 32 bytes of 32 rows; from this copy it
+ * reads one contiguous 256*bits-byte block, and each scale load one block of
+ * the tile's groups.  Layout, for expert e, 32-row tile t (rows past dims[1]
+ * zero) and K step kb of 64 values: data block (e, t, kb) of 256*bits bytes,
+ * lane l = 32h + r holding row r's codes 32h .. 32h+31 at byte 4*bits*l;
+ * scales (and biases) block (e, t, p) for the pair of steps p: 32 rows x
+ * (128/group_size) values, row-major.  All-null regions: no copy. */
+typedef struct {
+    moe_region data;
+    moe_region scales;
+    moe_region biases;
+} moe_packed_weight;
+
 /* FeedForward::Moe (crates/model-runtime/src/lib.rs:46-56) as bound by the
  * loader (crates/model-runtime/src/loader.rs:172-203).  has_shared = 0 admits
  * layers without a shared expert (Qwen3-30B-A3B style). */
@@ -191,7 +207,22 @@ typedef struct {
     uint32_t experts_used;      /* K, ModelConfig::experts_used (model-format/src/config.rs:42) */
     uint32_t normalize;         /* ModelConfig::normalize_expert_weights (config.rs:47) */
     uint32_t reserved;
+    /* optional MFMA tile-order copies of gate/up/down (moe_pack_weight); the
+     * bf16 MFMA path reads them when present (gate and up together) */
+    moe_packed_weight gate_packed;
+    moe_packed_weight up_packed;
+    moe_packed_weight down_packed;
 } moe_block_weights;
+
+/* Byte sizes of the packed copy of w (the codes; the scales and the biases
+ * each).  No reference counterpart.  MOE_ERR_SHAPE when w has no packed form:
+ * it must be affine with F16/BF16 scales, dims[0] a multiple of 128, and
+ * every byte offset of the copy below 2^32. */
+moe_status moe_pack_size(const moe_weight *w, uint64_t *data_bytes, uint64_t *sb_bytes);
+/* Batch op: writes the packed copy of w into `out`, whose regions must be
+ * owned by this gpu, not overlap w, and have the sizes above.  No reference
+ * counterpart (weight preparation for the prefill path). */
+moe_status moe_pack_weight(moe_gpu *gpu, const moe_weight *w, moe_packed_weight out);
 
 /* Path selection for moe_block. */
 enum {

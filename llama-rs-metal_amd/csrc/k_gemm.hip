@@ -131,6 +131,7 @@ struct Args {
     uint32_t n_tiles_n;        // N-tiles per M-tile
     uint32_t m_total;          // ROUTER: tokens
     uint32_t ksplit;           // ROUTER: K ranges (nk / ksplit is even)
+    PackedW pk, pk2;           // affine GATEUP/DOWN: MFMA tile-order copies of w, w2 (or nulls)
 };
 
 // Per-thread source of kBVals consecutive K values of one weight row: the code
@@ -469,9 +470,10 @@ __device__ __forceinline__ void codes8(const uint32_t *w, int j, float *c) {
 // step j to both operands.  GS = log2(group size) for 16-bit scales, whose
 // scale and bias loads then cover two K steps; 0 for F32 scales (one load
 // per step).
-template <int MODE, int BITS, int T, int NS, int GS>
+template <int MODE, int BITS, int T, int NS, int GS, bool PK>
 __device__ __forceinline__ void affine_item(const Args &a, uint8_t *abuf, uint32_t nt, uint32_t e,
                                             uint32_t m0, uint32_t seg_end, int lane, int wv) {
+    static_assert(!PK || GS != 0, "packed copies carry 16-bit scales");
     const int h = lane >> 5, l32 = lane & 31;
     const uint32_t in = a.w.in, out = a.w.out, nk = in / kTK;
     constexpr int ND = 2 * NS;  // DMA instructions per wave and step (8 rows each)
@@ -490,21 +492,35 @@ __device__ __forceinline__ void affine_item(const Args &a, uint8_t *abuf, uint32
     }
     // B: weight row n of tile t; rows past `out` read row 0 (never stored)
     uint32_t el0[kAfNT];  // element index of the lane's codes at K step 0 (< 2^32, host-checked)
+    // PK: byte offsets of the lane's codes at K step 0 and of its scales at
+    // step pair 0 in the packed copies (< 2^32, host-checked)
+    constexpr uint32_t kG2 = GS ? 128u >> GS : 1u;  // groups per row and step pair
+    uint32_t pko[kAfNT], pks[kAfNT];
+    const uint32_t ntile = (out + 31) / 32;
 #pragma unroll
     for (int t = 0; t < kAfNT; t++) {
         uint32_t n = MODE == GATEUP ? nt * (kTN / 2) + 32 * wv + l32 : nt * kTN + 64 * wv + 32 * t + l32;
+        const uint32_t tile = (e * ntile + n / 32);
+        pko[t] = tile * nk * (256 * BITS) + lane * (4 * BITS);
+        pks[t] = tile * (nk / 2) * (32 * kG2 * 2) + l32 * (kG2 * 2);
         if (n >= out) n = 0;
         el0[t] = (e * out + n) * in + 32 * h;
     }
     const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.a_rows);
-    const __amdgpu_buffer_rsrc_t rw[kAfNT] = {buffer_rsrc(a.w.data), buffer_rsrc(MODE == GATEUP ? a.w2.data : a.w.data)};
+    const void *wd[kAfNT] = {PK ? a.pk.data : a.w.data, PK ? (MODE == GATEUP ? a.pk2.data : a.pk.data)
+                                                              : (MODE == GATEUP ? a.w2.data : a.w.data)};
+    const void *ws[kAfNT] = {PK ? a.pk.scales : a.w.scales, PK ? (MODE == GATEUP ? a.pk2.scales : a.pk.scales)
+                                                                  : (MODE == GATEUP ? a.w2.scales : a.w.scales)};
+    const void *wb[kAfNT] = {PK ? a.pk.biases : a.w.biases, PK ? (MODE == GATEUP ? a.pk2.biases : a.pk.biases)
+                                                                  : (MODE == GATEUP ? a.w2.biases : a.w.biases)};
+    const __amdgpu_buffer_rsrc_t rw[kAfNT] = {buffer_rsrc(wd[0]), buffer_rsrc(wd[1])};
     // scale / bias arrays with their true sizes: the two-step loads may run
     // past the last group, and the hardware returns 0 there
-    const uint32_t sb_bytes = (uint32_t)(((uint64_t)a.w.experts * out * in >> a.w.gshift) * (T == 0 ? 4 : 2));
-    const __amdgpu_buffer_rsrc_t rs[kAfNT] = {buffer_rsrc(a.w.scales, sb_bytes),
-                                              buffer_rsrc(MODE == GATEUP ? a.w2.scales : a.w.scales, sb_bytes)};
-    const __amdgpu_buffer_rsrc_t rb[kAfNT] = {buffer_rsrc(a.w.biases, sb_bytes),
-                                              buffer_rsrc(MODE == GATEUP ? a.w2.biases : a.w.biases, sb_bytes)};
+    const uint32_t sb_bytes =
+        PK ? (uint32_t)((uint64_t)a.w.experts * ntile * (nk / 2) * (32 * kG2 * 2))
+           : (uint32_t)(((uint64_t)a.w.experts * out * in >> a.w.gshift) * (T == 0 ? 4 : 2));
+    const __amdgpu_buffer_rsrc_t rs[kAfNT] = {buffer_rsrc(ws[0], sb_bytes), buffer_rsrc(ws[1], sb_bytes)};
+    const __amdgpu_buffer_rsrc_t rb[kAfNT] = {buffer_rsrc(wb[0], sb_bytes), buffer_rsrc(wb[1], sb_bytes)};
     const uint32_t gshift = a.w.gshift;
 
     f32x16 acc[NS][kAfNT];
@@ -525,7 +541,7 @@ __device__ __forceinline__ void affine_item(const Args &a, uint8_t *abuf, uint32
     auto load_b = [&](AfStage<BITS> &st, uint32_t kb) {
 #pragma unroll
         for (int t = 0; t < kAfNT; t++) {
-            const uint32_t vo = el0[t] / (8 / BITS), so = kb * (8 * BITS);
+            const uint32_t vo = PK ? pko[t] : el0[t] / (8 / BITS), so = kb * (PK ? 256 * BITS : 8 * BITS);
             if constexpr (BITS == 2) {
                 const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rw[t], vo, so, 0);
                 st.w[t][0] = v[0];
@@ -557,13 +573,32 @@ __device__ __forceinline__ void affine_item(const Args &a, uint8_t *abuf, uint32
         if constexpr (GS != 0) {
 #pragma unroll
             for (int t = 0; t < kAfNT; t++) {
-                const uint32_t g = ((el0[t] - 32 * h + kb * kTK) >> GS) & ~1u;
-                const u32x2 vs = __builtin_amdgcn_raw_buffer_load_b64(rs[t], g * 2, 0, 0);
-                const u32x2 vb = __builtin_amdgcn_raw_buffer_load_b64(rb[t], g * 2, 0, 0);
-                sc2.s[t][0] = vs[0];
-                sc2.s[t][1] = vs[1];
-                sc2.b[t][0] = vb[0];
-                sc2.b[t][1] = vb[1];
+                if constexpr (PK) {
+                    // the tile's block for step pair kb / 2: this row's kG2 values
+                    const uint32_t so = (kb / 2) * (32 * kG2 * 2);
+                    if constexpr (GS == 5) {
+                        const u32x2 vs = __builtin_amdgcn_raw_buffer_load_b64(rs[t], pks[t], so, 0);
+                        const u32x2 vb = __builtin_amdgcn_raw_buffer_load_b64(rb[t], pks[t], so, 0);
+                        sc2.s[t][0] = vs[0];
+                        sc2.s[t][1] = vs[1];
+                        sc2.b[t][0] = vb[0];
+                        sc2.b[t][1] = vb[1];
+                    } else if constexpr (GS == 6) {
+                        sc2.s[t][0] = __builtin_amdgcn_raw_buffer_load_b32(rs[t], pks[t], so, 0);
+                        sc2.b[t][0] = __builtin_amdgcn_raw_buffer_load_b32(rb[t], pks[t], so, 0);
+                    } else {
+                        sc2.s[t][0] = __builtin_amdgcn_raw_buffer_load_b16(rs[t], pks[t], so, 0);
+                        sc2.b[t][0] = __builtin_amdgcn_raw_buffer_load_b16(rb[t], pks[t], so, 0);
+                    }
+                } else {
+                    const uint32_t g = ((el0[t] - 32 * h + kb * kTK) >> GS) & ~1u;
+                    const u32x2 vs = __builtin_amdgcn_raw_buffer_load_b64(rs[t], g * 2, 0, 0);
+                    const u32x2 vb = __builtin_amdgcn_raw_buffer_load_b64(rb[t], g * 2, 0, 0);
+                    sc2.s[t][0] = vs[0];
+                    sc2.s[t][1] = vs[1];
+                    sc2.b[t][0] = vb[0];
+                    sc2.b[t][1] = vb[1];
+                }
             }
         }
     };
@@ -572,6 +607,7 @@ __device__ __forceinline__ void affine_item(const Args &a, uint8_t *abuf, uint32
     auto pick = [&](const uint32_t *pair, int t, int s, uint32_t kb) -> uint32_t {
         if constexpr (GS == 5) return pair[s] >> (16 * h);
         else if constexpr (GS == 6) return pair[0] >> (16 * s);
+        else if constexpr (PK) return pair[0];
         else return pair[0] >> (16 * (((el0[t] - 32 * h + kb * kTK) >> 7) & 1));
     };
     auto compute = [&](const uint8_t *cur, const AfStage<BITS> &sc, const AfScales &sc2, int s2, uint32_t kb) {
@@ -668,14 +704,14 @@ __device__ __forceinline__ void affine_item(const Args &a, uint8_t *abuf, uint32
     }
 }
 
-template <int MODE, int BITS, int T, int GS>
+template <int MODE, int BITS, int T, int GS, bool PK>
 __device__ __forceinline__ void affine_live(const Args &a, uint8_t *abuf, uint32_t nt, uint32_t e,
                                             uint32_t m0, uint32_t seg_end, uint32_t live, int lane,
                                             int wv) {
-    if (live > 96) affine_item<MODE, BITS, T, 4, GS>(a, abuf, nt, e, m0, seg_end, lane, wv);
-    else if (live > 64) affine_item<MODE, BITS, T, 3, GS>(a, abuf, nt, e, m0, seg_end, lane, wv);
-    else if (live > 32) affine_item<MODE, BITS, T, 2, GS>(a, abuf, nt, e, m0, seg_end, lane, wv);
-    else affine_item<MODE, BITS, T, 1, GS>(a, abuf, nt, e, m0, seg_end, lane, wv);
+    if (live > 96) affine_item<MODE, BITS, T, 4, GS, PK>(a, abuf, nt, e, m0, seg_end, lane, wv);
+    else if (live > 64) affine_item<MODE, BITS, T, 3, GS, PK>(a, abuf, nt, e, m0, seg_end, lane, wv);
+    else if (live > 32) affine_item<MODE, BITS, T, 2, GS, PK>(a, abuf, nt, e, m0, seg_end, lane, wv);
+    else affine_item<MODE, BITS, T, 1, GS, PK>(a, abuf, nt, e, m0, seg_end, lane, wv);
 }
 
 // Affine GATEUP / DOWN products: same persistent XCD-range schedule as
@@ -698,11 +734,15 @@ void affine_gemm_kernel(Args a) {
         const uint32_t seg_end = a.offsets[e + 1];
         const uint32_t live = min(seg_end - m0, (uint32_t)kTM);
         if constexpr (T == 0) {
-            affine_live<MODE, BITS, T, 0>(a, abuf, nt, e, m0, seg_end, live, lane, wv);
+            affine_live<MODE, BITS, T, 0, false>(a, abuf, nt, e, m0, seg_end, live, lane, wv);
+        } else if (a.pk.data) {
+            if (a.w.gshift == 5) affine_live<MODE, BITS, T, 5, true>(a, abuf, nt, e, m0, seg_end, live, lane, wv);
+            else if (a.w.gshift == 6) affine_live<MODE, BITS, T, 6, true>(a, abuf, nt, e, m0, seg_end, live, lane, wv);
+            else affine_live<MODE, BITS, T, 7, true>(a, abuf, nt, e, m0, seg_end, live, lane, wv);
         } else {
-            if (a.w.gshift == 5) affine_live<MODE, BITS, T, 5>(a, abuf, nt, e, m0, seg_end, live, lane, wv);
-            else if (a.w.gshift == 6) affine_live<MODE, BITS, T, 6>(a, abuf, nt, e, m0, seg_end, live, lane, wv);
-            else affine_live<MODE, BITS, T, 7>(a, abuf, nt, e, m0, seg_end, live, lane, wv);
+            if (a.w.gshift == 5) affine_live<MODE, BITS, T, 5, false>(a, abuf, nt, e, m0, seg_end, live, lane, wv);
+            else if (a.w.gshift == 6) affine_live<MODE, BITS, T, 6, false>(a, abuf, nt, e, m0, seg_end, live, lane, wv);
+            else affine_live<MODE, BITS, T, 7, false>(a, abuf, nt, e, m0, seg_end, live, lane, wv);
         }
     }
 }
@@ -766,9 +806,10 @@ struct SetLds {
 };
 
 hipError_t launch_grouped_gemm(Prof *p, hipStream_t s, int down, const WDesc &w, const WDesc &w2,
-                               const uint16_t *a_rows, uint64_t a_rows_n, const uint32_t *perm,
-                               const uint32_t *offsets, const uint32_t *tiles, const uint32_t *ntiles,
-                               uint32_t k, uint16_t *out) {
+                               const PackedW &pk, const PackedW &pk2, const uint16_t *a_rows,
+                               uint64_t a_rows_n, const uint32_t *perm, const uint32_t *offsets,
+                               const uint32_t *tiles, const uint32_t *ntiles, uint32_t k,
+                               uint16_t *out) {
     gemm::Args a{};
     a.w = w;
     a.w2 = w2;
@@ -783,6 +824,11 @@ hipError_t launch_grouped_gemm(Prof *p, hipStream_t s, int down, const WDesc &w,
     const bool affine = affine_fits(w, a_rows_n) && affine_fits(w2, a_rows_n) && w2.bits == w.bits &&
                         w2.type == w.type && w2.gshift == w.gshift;
     const uint32_t affine_blocks = gemm_blocks(gemm::kAfBlocksPerCu);
+    // the packed copies are read when both operands have one (16-bit scales)
+    if (affine && w.type != 0 && pk.data && pk2.data) {
+        a.pk = pk;
+        a.pk2 = pk2;
+    }
     hipError_t e;
     if (down) {
         a.n_tiles_n = (w.out + gemm::kTN - 1) / gemm::kTN;

@@ -174,17 +174,19 @@ hipError_t launch_tile_schedule(Prof *p, hipStream_t s, const uint32_t *offsets,
 }
 
 hipError_t launch_mfma_experts(Prof *p, hipStream_t s, const WDesc &gate, const WDesc &up,
-                               const WDesc &down, const uint16_t *xb16, uint32_t tokens,
+                               const WDesc &down, const PackedW &pg, const PackedW &pu,
+                               const PackedW &pd, const uint16_t *xb16, uint32_t tokens,
                                const uint32_t *offsets, const uint32_t *perm, uint32_t k,
                                uint32_t *tiles, uint32_t *ntiles, uint16_t *act16, uint16_t *y16) {
     const uint32_t E = gate.experts;
     hipError_t e = launch_kernel(p, "tile_schedule", tile_schedule_kernel, dim3(1), dim3(64), 0, s,
                                  offsets, E, gemm_tile_rows(), tiles, ntiles);
     if (e != hipSuccess) return e;
-    e = launch_grouped_gemm(p, s, 0, gate, up, xb16, tokens, perm, offsets, tiles, ntiles, k, act16);
+    e = launch_grouped_gemm(p, s, 0, gate, up, pg, pu, xb16, tokens, perm, offsets, tiles, ntiles, k,
+                            act16);
     if (e != hipSuccess) return e;
-    return launch_grouped_gemm(p, s, 1, down, down, act16, (uint64_t)tokens * k, perm, offsets, tiles,
-                               ntiles, k, y16);
+    return launch_grouped_gemm(p, s, 1, down, down, pd, pd, act16, (uint64_t)tokens * k, perm, offsets,
+                               tiles, ntiles, k, y16);
 }
 
 // Same combine with 8 columns per thread (16-byte row loads, all K rows of a

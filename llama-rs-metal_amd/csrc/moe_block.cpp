@@ -98,7 +98,24 @@ moe_status check_block(moe_gpu *g, const moe_block_weights *w, Dims &d) {
             return shape(g, "shared expert gate dimensions");
     }
     if (d.E > 16384) return shape(g, "more than 16384 experts");
+    // optional packed copies: sized for their weight, owned, disjoint from it
+    const moe_packed_weight *pk[3] = {&w->gate_packed, &w->up_packed, &w->down_packed};
+    const moe_weight *pw[3] = {&w->gate, &w->up, &w->down};
+    for (int i = 0; i < 3; i++) {
+        if (!pk[i]->data.ptr && !pk[i]->scales.ptr && !pk[i]->biases.ptr) continue;
+        uint64_t db = 0, sb = 0;
+        if (!pack_layout(wdesc(*pw[i]), &db, &sb) || pk[i]->data.bytes != db || pk[i]->scales.bytes != sb ||
+            pk[i]->biases.bytes != sb)
+            return shape(g, "packed expert weight: no packed form, or sizes");
+        if ((st = check_own(g, {rng(pk[i]->data), rng(pk[i]->scales), rng(pk[i]->biases)}))) return st;
+    }
+    if (!w->gate_packed.data.ptr != !w->up_packed.data.ptr)
+        return shape(g, "packed expert weights: gate and up together");
     return MOE_OK;
+}
+
+PackedW packed(const moe_packed_weight &p) {
+    return PackedW{p.data.ptr, p.scales.ptr, p.biases.ptr};
 }
 
 float *fp(const moe_buffer &b, uint64_t off = 0) { return static_cast<float *>(b.ptr) + off; }
@@ -297,8 +314,9 @@ moe_status run_mfma(moe_gpu *g, const moe_block_weights *w, const Dims &d, const
         TRY(launch_route(p, s, logits, E, K, w->normalize ? 1 : 0, (uint32_t)T, ids, wts));
     }
     TRY(launch_dispatch(p, s, ids, (uint32_t)(T * K), E, counts, offsets, perm, pos));
-    TRY(launch_mfma_experts(p, s, wdesc(w->gate), wdesc(w->up), wdesc(w->down), xb16, (uint32_t)T,
-                            offsets, perm, K, tiles, ntiles, act16, y16));
+    TRY(launch_mfma_experts(p, s, wdesc(w->gate), wdesc(w->up), wdesc(w->down), packed(w->gate_packed),
+                            packed(w->up_packed), packed(w->down_packed), xb16, (uint32_t)T, offsets, perm,
+                            K, tiles, ntiles, act16, y16));
     const float *so = nullptr, *sgv = nullptr;
     if (w->has_shared) {
         float *sg = ws + L.sh_act, *su = ws + L.sh_up, *sout = ws + L.sh_out, *sgt = ws + L.sh_gate;
@@ -318,6 +336,31 @@ moe_status run_mfma(moe_gpu *g, const moe_block_weights *w, const Dims &d, const
 }  // namespace
 
 extern "C" {
+
+moe_status moe_pack_size(const moe_weight *w, uint64_t *data_bytes, uint64_t *sb_bytes) {
+    if (!w || !data_bytes || !sb_bytes || w->ndims == 0 || w->ndims > 3 || w->bits == 0 ||
+        (w->group_size != 32 && w->group_size != 64 && w->group_size != 128))
+        return MOE_ERR_SHAPE;
+    for (uint32_t i = 0; i < w->ndims; i++)
+        if (w->dims[i] == 0 || !fits_u32(w->dims[i])) return MOE_ERR_SHAPE;
+    return pack_layout(wdesc(*w), data_bytes, sb_bytes) ? MOE_OK : MOE_ERR_SHAPE;
+}
+
+moe_status moe_pack_weight(moe_gpu *g, const moe_weight *w, moe_packed_weight out) {
+    moe_status st = need_batch(g);
+    if (st) return st;
+    if ((st = check_weight(g, w, "pack weight"))) return st;
+    uint64_t db = 0, sb = 0;
+    if (moe_pack_size(w, &db, &sb) != MOE_OK) return shape(g, "pack weight: no packed form");
+    if (out.data.bytes != db || out.scales.bytes != sb || out.biases.bytes != sb)
+        return shape(g, "pack weight: packed region sizes");
+    if ((st = check_own(g, {rng(out.data), rng(out.scales), rng(out.biases)}))) return st;
+    if ((st = check_alias(g, weight_ranges(*w), {rng(out.data), rng(out.scales), rng(out.biases)}, false)))
+        return st;
+    return launched(g, launch_pack_weight(&g->prof, g->stream, wdesc(*w), const_cast<void *>(out.data.ptr),
+                                          const_cast<void *>(out.scales.ptr), const_cast<void *>(out.biases.ptr)),
+                    "pack weight");
+}
 
 moe_status moe_block_workspace(const moe_block_weights *w, uint64_t tokens, uint64_t *elems) {
     if (!w || !elems || tokens == 0) return MOE_ERR_SHAPE;

@@ -130,8 +130,23 @@ hipError_t launch_grouped_down(Prof *p, hipStream_t s, const WDesc &down, const 
 // ---- prefill around the bf16 MFMA GEMMs (k_mfma.hip) ----
 hipError_t launch_to_bf16(Prof *p, hipStream_t s, const float *x, const float *norm_w, float eps,
                           uint32_t tokens, uint32_t h, uint16_t *y, float *xn);
+// An affine expert weight repacked in MFMA tile order (k_pack.hip): for
+// expert e, 32-row tile t (rows past `out` zero) and K step kb (64 values),
+// the 32 rows' codes form one block of 256*BITS bytes in which lane
+// l = 32h + r holds row r's codes 32h .. 32h + 31 at byte 4*BITS*l; for each
+// pair of K steps p, the tile's scales (and biases) form one block of
+// 32 rows x (128 >> gshift) 16-bit values, row-major.  Null data: no copy.
+struct PackedW {
+    const void *data, *scales, *biases;
+};
+// Byte sizes of the packed copy (false: no packed form -- affine weights with
+// 16-bit scales, in % 128 == 0, offsets below 2^32 only).
+bool pack_layout(const WDesc &w, uint64_t *data_bytes, uint64_t *sb_bytes);
+hipError_t launch_pack_weight(Prof *p, hipStream_t s, const WDesc &w, void *data, void *scales,
+                              void *biases);
 hipError_t launch_mfma_experts(Prof *p, hipStream_t s, const WDesc &gate, const WDesc &up,
-                               const WDesc &down, const uint16_t *xb16, uint32_t tokens,
+                               const WDesc &down, const PackedW &pg, const PackedW &pu,
+                               const PackedW &pd, const uint16_t *xb16, uint32_t tokens,
                                const uint32_t *offsets, const uint32_t *perm, uint32_t k,
                                uint32_t *tiles, uint32_t *ntiles, uint16_t *act16, uint16_t *y16);
 // Grouped expert GEMM over the dispatched segments (k_gemm.hip): down = 0 for
@@ -142,10 +157,12 @@ hipError_t launch_mfma_experts(Prof *p, hipStream_t s, const WDesc &gate, const 
 // tile_schedule.
 bool gemm_supported(const WDesc &w);
 uint32_t gemm_tile_rows();  // pairs per work item (the M-tiles tile_schedule emits)
+// pk, pk2: packed copies of w, w2 (PackedW with null data: none).
 hipError_t launch_grouped_gemm(Prof *p, hipStream_t s, int down, const WDesc &w, const WDesc &w2,
-                               const uint16_t *a_rows, uint64_t a_rows_n, const uint32_t *perm,
-                               const uint32_t *offsets, const uint32_t *tiles, const uint32_t *ntiles,
-                               uint32_t k, uint16_t *out);
+                               const PackedW &pk, const PackedW &pk2, const uint16_t *a_rows,
+                               uint64_t a_rows_n, const uint32_t *perm, const uint32_t *offsets,
+                               const uint32_t *tiles, const uint32_t *ntiles, uint32_t k,
+                               uint16_t *out);
 hipError_t launch_combine16(Prof *p, hipStream_t s, const uint16_t *y16, const uint32_t *pos,
                             const float *wts, uint32_t k, const float *sh_out, const float *sh_gate,
                             const float *resid, float *out, uint32_t tokens, uint32_t h);

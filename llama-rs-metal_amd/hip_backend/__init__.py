@@ -4,11 +4,12 @@
 `synth` builds the seeded synthetic inputs of the benchmark configurations.
 """
 from .api import (BF16, F16, F32, PATH_AUTO, PATH_GROUPED, PATH_MFMA, PATH_OPS, SIGNATURES, AllocationError,
-                  Batch, BlockWeights, Buffer, Gpu, GpuError, MoeError, ShapeError, Tensor,
-                  UnavailableError, Weight, load_library, LIB_PATH)
+                  Batch, BlockWeights, Buffer, Gpu, GpuError, MoeError, PackedWeight, ShapeError, Tensor,
+                  UnavailableError, Weight, load_library, pack_size, LIB_PATH)
 
 __all__ = [
     "BF16", "F16", "F32", "PATH_AUTO", "PATH_GROUPED", "PATH_MFMA", "PATH_OPS", "SIGNATURES",
     "AllocationError", "Batch", "BlockWeights", "Buffer", "Gpu", "GpuError", "MoeError",
-    "ShapeError", "Tensor", "UnavailableError", "Weight", "load_library", "LIB_PATH",
+    "PackedWeight", "ShapeError", "Tensor", "UnavailableError", "Weight", "load_library", "pack_size",
+    "LIB_PATH",
 ]

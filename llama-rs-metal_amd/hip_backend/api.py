@@ -74,6 +74,10 @@ class MoeWeightC(C.Structure):
     ]
 
 
+class MoePackedWeightC(C.Structure):
+    _fields_ = [("data", MoeRegionC), ("scales", MoeRegionC), ("biases", MoeRegionC)]
+
+
 class MoeBlockWeightsC(C.Structure):
     _fields_ = [
         ("router", MoeWeightC),
@@ -88,6 +92,9 @@ class MoeBlockWeightsC(C.Structure):
         ("experts_used", C.c_uint32),
         ("normalize", C.c_uint32),
         ("reserved", C.c_uint32),
+        ("gate_packed", MoePackedWeightC),
+        ("up_packed", MoePackedWeightC),
+        ("down_packed", MoePackedWeightC),
     ]
 
 
@@ -137,6 +144,8 @@ SIGNATURES = {
     "moe_norm": (I32, [P, BUF, C.POINTER(MoeWeightC), BUF, U64, U64, F]),
     "moe_route_tokens": (I32, [P, BUF, BUF, BUF, U64, I32]),
     "moe_dispatch": (I32, [P, BUF, U64, U64, U64, BUF, BUF, BUF, BUF]),
+    "moe_pack_size": (I32, [C.POINTER(MoeWeightC), C.POINTER(U64), C.POINTER(U64)]),
+    "moe_pack_weight": (I32, [P, C.POINTER(MoeWeightC), MoePackedWeightC]),
     "moe_block_workspace": (I32, [C.POINTER(MoeBlockWeightsC), U64, C.POINTER(U64)]),
     "moe_block": (I32, [P, C.POINTER(MoeBlockWeightsC), BUF, BUF, U64, C.POINTER(MoeBlockIOC)]),
     "moe_profile_enable": (I32, [P, I32]),
@@ -254,6 +263,24 @@ class Weight:
         return Weight(c, self.regions, dims, self.bits)
 
 
+class PackedWeight:
+    """MFMA tile-order copy of an affine expert weight (moe_pack_weight; no
+    reference counterpart): its three device buffers and the C struct."""
+
+    def __init__(self, c, buffers):
+        self.c = c
+        self.buffers = buffers
+
+
+def pack_size(weight):
+    """(code bytes, scale-or-bias bytes) of the packed copy of `weight`, or
+    None when it has no packed form."""
+    db, sb = C.c_uint64(), C.c_uint64()
+    if _lib.moe_pack_size(C.byref(weight.c), C.byref(db), C.byref(sb)) != 0:
+        return None
+    return int(db.value), int(sb.value)
+
+
 def _empty_weight():
     return MoeWeightC()
 
@@ -262,9 +289,13 @@ class BlockWeights:
     """FeedForward::Moe (crates/model-runtime/src/lib.rs:46-56)."""
 
     def __init__(self, router, gate, up, down, experts_used, normalize, shared=None,
-                 shared_gate=None):
+                 shared_gate=None, packed=None):
         c = MoeBlockWeightsC()
         c.router, c.gate, c.up, c.down = router.c, gate.c, up.c, down.c
+        if packed is not None:  # PackedWeight copies of (gate, up, down), any of them None
+            for name, pw in zip(("gate_packed", "up_packed", "down_packed"), packed):
+                if pw is not None:
+                    setattr(c, name, pw.c)
         if shared is not None:
             c.shared_gate, c.shared_up, c.shared_down = shared[0].c, shared[1].c, shared[2].c
             c.shared_gate_inp = shared_gate.c
@@ -273,6 +304,7 @@ class BlockWeights:
         c.normalize = int(bool(normalize))
         self.c = c
         self.keep = (router, gate, up, down, shared, shared_gate)
+        self.packed = packed
         self.hidden = router.dims[0]
         self.experts = router.dims[1]
         self.k = experts_used
@@ -388,6 +420,24 @@ class Gpu:
         for i, d in enumerate(t.dims):
             c.dims[i] = d
         return Weight(c, regions, t.dims, t.bits)
+
+    def pack_weight(self, weight):
+        """Allocate and fill the packed copy of `weight` (one batch); None
+        when it has no packed form."""
+        sizes = pack_size(weight)
+        if sizes is None:
+            return None
+        db, sb = sizes
+        bufs = [self.zeros(db // 4), self.zeros(sb // 4), self.zeros(sb // 4)]
+        c = MoePackedWeightC()
+        for name, b, n in zip(("data", "scales", "biases"), bufs, (db, sb, sb)):
+            r = MoeRegionC()
+            r.ptr, r.bytes = b.c.ptr, n
+            setattr(c, name, r)
+        pw = PackedWeight(c, bufs)
+        with self.batch() as b:
+            b.pack_weight(weight, pw)
+        return pw
 
     def weight_f32(self, data, dims):
         return self.weight_tensor(Tensor.dense(dims, np.asarray(data, np.float32)))
@@ -535,6 +585,9 @@ class Batch:
 
     def copy(self, src, dst):
         self._ck(_lib.moe_copy(self.gpu._h, src.c, dst.c))
+
+    def pack_weight(self, weight, packed):
+        _check(self.gpu, _lib.moe_pack_weight(self.gpu._h, C.byref(weight.c), packed.c))
 
     def moe_block(self, bw, x, out, tokens, workspace, logit_bias=None, logits_out=None,
                   ids_out=None, weights_out=None, norm_weight=None, norm_eps=1e-6,

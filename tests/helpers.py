@@ -143,3 +143,30 @@ def close(a, b, tol=5e-4):
     bad = np.abs(a - b) >= tol * (1 + np.abs(b))
     assert not bad.any(), f"{int(bad.sum())} mismatches, first {np.argwhere(bad)[:3].ravel()}: " \
                           f"{a[bad][:3]} != {b[bad][:3]}"
+
+
+# ----------------------------------------------------------- packed layout --
+def pack_reference(t):
+    """The MFMA tile-order copy of affine tensor t (dims [in, out, E]) as
+    (codes uint32, scales uint16, biases uint16) -- the layout documented at
+    moe_packed_weight in include/moe_hip.h, restated with numpy: block
+    (e, tile, kb) holds lanes l = 32h + r in order, lane l the `bits` words of
+    row 32*tile + r covering codes 64*kb + 32h .. +32; block (e, tile, p) of
+    the scales holds rows r = 0..31, each its 128/group values of the step
+    pair p.  Rows past `out` are zero."""
+    in_, out = t.dims[0], t.dims[1]
+    E = t.dims[2] if len(t.dims) > 2 else 1
+    bits, gs = t.bits, t.group_size
+    ntile, nk = (out + 31) // 32, in_ // 64
+    wpr = in_ * bits // 32
+    words = np.zeros((E, ntile * 32, wpr), np.uint32)
+    words[:, :out] = np.asarray(t.data, np.uint32).reshape(E, out, wpr)
+    codes = words.reshape(E, ntile, 32, nk, 2, bits).transpose(0, 1, 3, 4, 2, 5).ravel()
+    G, g2 = in_ // gs, 128 // gs
+
+    def groups(a):
+        v = np.zeros((E, ntile * 32, G), np.uint16)
+        v[:, :out] = np.asarray(a).view(np.uint16).reshape(E, out, G)
+        return v.reshape(E, ntile, 32, nk // 2, g2).transpose(0, 1, 3, 2, 4).ravel()
+
+    return codes, groups(t.scales), groups(t.biases)

@@ -85,3 +85,30 @@ def test_null_handles_are_rejected():
     assert lib.moe_batch_begin(None) == 3
     assert lib.moe_profile_enable(None, 1) == 3
     assert lib.moe_allocated_bytes(None) == 0
+
+
+def test_pack_size_is_host_only():
+    """moe_pack_size: the MFMA tile-order copy's sizes from the weight's
+    metadata alone (32-row tiles, rows padded; 64-value K steps of 256*bits
+    bytes; per pair of steps 32 x 128/group 16-bit values), and no packed form
+    for dense weights, F32 scales or rows not a multiple of 128."""
+    lib = api.load_library()
+
+    def w(dims, bits, group, st):
+        c = api.MoeWeightC()
+        c.ndims = len(dims)
+        for i, d in enumerate(dims):
+            c.dims[i] = d
+        c.bits, c.group_size, c.scale_type = bits, group, st
+        return c
+
+    db, sb = C.c_uint64(), C.c_uint64()
+    for dims, bits, group in [([2048, 768, 128], 4, 64), ([768, 2048, 128], 8, 32),
+                              ([256, 40, 3], 2, 128)]:
+        assert lib.moe_pack_size(C.byref(w(dims, bits, group, api.BF16)), C.byref(db), C.byref(sb)) == 0
+        ntile, nk = (dims[1] + 31) // 32, dims[0] // 64
+        assert db.value == dims[2] * ntile * nk * 256 * bits
+        assert sb.value == dims[2] * ntile * (nk // 2) * 32 * (128 // group) * 2
+    for c in [w([2048, 768, 128], 4, 64, api.F32), w([2048, 768, 128], 0, 0, 0),
+              w([192, 64, 2], 4, 64, api.BF16)]:
+        assert lib.moe_pack_size(C.byref(c), C.byref(db), C.byref(sb)) == 3

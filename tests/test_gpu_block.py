@@ -11,7 +11,7 @@ import pytest
 
 import oracle
 from helpers import (DENSE, HostBlock, close, config1, config2, config3, config4, config5, hot_bias,
-                     rel_max_err, zipf_bias)
+                     pack_reference, rel_max_err, zipf_bias)
 from hip_backend import (BF16, F16, F32, PATH_AUTO, PATH_GROUPED, PATH_MFMA, PATH_OPS, BlockWeights,
                          Tensor, synth)
 
@@ -369,6 +369,46 @@ def test_mfma_experts_all_affine_layouts(gpu, bits, group, st):
               for m in range(0, int(c), 128)}
     assert slices >= {1, 2, 3, 4}
     check_against_oracle(blk, x, got, tokens=range(0, T, 7), bias=bias, tol=BF16_TOL,
+                         logit_tol=BF16_TOL)
+
+
+@pytest.mark.parametrize("dims,bits,group,st", [([256, 40, 3], 2, 128, F16), ([256, 64, 2], 4, 64, BF16),
+                                                 ([128, 96, 2], 8, 32, BF16), ([384, 33, 1], 4, 32, F16)])
+def test_pack_weight_layout(gpu, dims, bits, group, st):
+    """moe_pack_weight writes the documented MFMA tile-order layout (compared
+    word for word with its numpy restatement), rows past `out` zero."""
+    print(f"[case] pack layout dims={dims} bits={bits} group={group}", flush=True)
+    t = Tensor.affine(dims, *synth.random_affine(7700 + bits, int(np.prod(dims)), bits, group, st), bits,
+                      group, st)
+    pw = gpu.pack_weight(gpu.weight_tensor(t))
+    codes, scales, biases = pack_reference(t)
+    assert np.array_equal(gpu.read(pw.buffers[0]).view(np.uint32), codes)
+    assert np.array_equal(gpu.read(pw.buffers[1]).view(np.uint16), scales)
+    assert np.array_equal(gpu.read(pw.buffers[2]).view(np.uint16), biases)
+
+
+@pytest.mark.parametrize("bits,group,st", [(2, 32, BF16), (4, 64, F16), (4, 128, BF16), (8, 64, BF16),
+                                           (8, 128, F16)])
+def test_mfma_packed_matches_unpacked(gpu, bits, group, st):
+    """The MFMA path over packed copies of gate/up/down computes exactly what
+    it computes over the row-major tensors (same products, same order), and
+    both match the oracle to the bf16 tolerance."""
+    print(f"[case] MFMA packed bits={bits} group={group} st={st}", flush=True)
+    blk = HostBlock(256, 8, 2, 128, 0, {"router": DENSE, "experts": (bits, group, st)},
+                    seed=80 + bits, random_experts=True)
+    bw = blk.upload(gpu)
+    router, gate, up, down = bw.keep[:4]
+    packed = [gpu.pack_weight(w) for w in (gate, up, down)]
+    assert all(p is not None for p in packed)
+    bwp = BlockWeights(router, gate, up, down, bw.k, True, packed=packed)
+    T = 300
+    x = synth.normal(4500 + bits, T * 256).reshape(T, 256)
+    bias = zipf_bias(T, 8, seed=1, s=0.5)
+    got = run_block(gpu, bw, x, T, PATH_MFMA, bias=bias)
+    gotp = run_block(gpu, bwp, x, T, PATH_MFMA, bias=bias)
+    assert np.array_equal(got[2], gotp[2])
+    assert np.array_equal(got[0], gotp[0])
+    check_against_oracle(blk, x, gotp, tokens=range(0, T, 11), bias=bias, tol=BF16_TOL,
                          logit_tol=BF16_TOL)
 
 
