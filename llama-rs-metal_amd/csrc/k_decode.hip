@@ -17,6 +17,7 @@ namespace moehip {
 struct DecodeKArgs {
     WDesc router, gate, up, down, sg, su, sd, sgi;
     uint32_t has_shared, k, normalize;
+    uint32_t down_slots;  // decode_down stages each wave's activation row in LDS
     uint32_t h, ff, ffs, E;
     uint32_t lpr_h, lpr_f;  // lanes per row along h / along ff (powers of two <= 64)
     uint32_t n_router_waves, n_shared_waves, n_gate_waves_per_expert;
@@ -183,15 +184,47 @@ __global__ __launch_bounds__(64) void decode_gateup_kernel(DecodeKArgs a) {
 // ------------------------------------------------------------------ down --
 // Block = nw waves over `rows_per_block` output rows; wave w takes experts
 // w, w+nw, ... of the K routed experts plus the shared one (index K); all of
-// a wave's loads are issued before its arithmetic, and the waves' partial
-// sums meet in LDS.
+// a wave's weight loads are issued before its arithmetic, its expert's
+// activation row reaches every sub-wave through the wave's LDS slot
+// (staged_row), and the waves' partial sums meet in LDS.
 constexpr int kDownMaxWaves = 16;
 constexpr int kDownMaxPerWave = 2;
+constexpr size_t kDownSlotBytes = 48 * 1024;  // beside the 16 KiB combine arrays
+
+// This wave's activation row (ff floats) into xr: with a slot, through the
+// wave's own LDS slot -- lane l loads float4s l, l + 64, ... once and every
+// sub-wave reads its chunk from LDS (float4 i of chunk c at slot i * C + c,
+// so a sub-wave's 16 lanes read consecutive slots); the direct loads fetched
+// the row once per sub-wave (64 / lpr times).  Without a slot (rows too long
+// for the block's LDS), direct loads.
+__device__ __forceinline__ void staged_row(float4 *slot, const float *src, uint32_t ff, int lane,
+                                           uint32_t cl, float *xr) {
+    if (!slot) {
+        XChunk X;
+        X.load(src, nullptr, cl);
+#pragma unroll
+        for (int j = 0; j < 32; j++) xr[j] = X.xr[j];
+        return;
+    }
+    const uint32_t C = ff / 32, n4 = ff / 4;
+    const float4 *s4 = reinterpret_cast<const float4 *>(src);
+    for (uint32_t w4 = lane; w4 < n4; w4 += 64) slot[(w4 % 8) * C + w4 / 8] = s4[w4];
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 v = slot[i * C + cl];
+        xr[4 * i + 0] = v.x;
+        xr[4 * i + 1] = v.y;
+        xr[4 * i + 2] = v.z;
+        xr[4 * i + 3] = v.w;
+    }
+}
 
 template <int BITS, int ST, int BS>
 __device__ __forceinline__ void down_wave(const DecodeKArgs &a, uint32_t wv, uint32_t nw,
                                           uint32_t row0, uint32_t sub, uint32_t cl, uint32_t rpi,
-                                          float *acc_r, float *acc_s) {
+                                          float4 *slot, float *acc_r, float *acc_s) {
     const uint32_t n_exp = a.k + (a.has_shared ? 1u : 0u);
     const uint32_t C = a.ff / 32;
 #pragma unroll
@@ -205,7 +238,6 @@ __device__ __forceinline__ void down_wave(const DecodeKArgs &a, uint32_t wv, uin
         if (kk < a.k) {
             const uint32_t e = a.ids[kk];
             const float wk = a.weights[kk];
-            X.load(a.act + (uint64_t)kk * a.ff, nullptr, cl);
 #pragma unroll
             for (int f = 0; f < kDownFR; f++) {
                 const uint32_t r = row0 + f * rpi + sub;
@@ -215,11 +247,11 @@ __device__ __forceinline__ void down_wave(const DecodeKArgs &a, uint32_t wv, uin
             LaneRows<BITS, ST, kDownFR> L;
             L.load(a.down, rows, ok, cl, C);
             loads_issued();
+            staged_row(slot, a.act + (uint64_t)kk * a.ff, a.ff, (int)(threadIdx.x & 63), cl, X.xr);
             L.dot(X.xr, X.finish(nullptr, 0.f, 0, 0), part);
 #pragma unroll
             for (int f = 0; f < kDownFR; f++) acc_r[f] += part[f] * wk;
         } else {
-            X.load(a.sh_act, nullptr, cl);
 #pragma unroll
             for (int f = 0; f < kDownFR; f++) {
                 const uint32_t r = row0 + f * rpi + sub;
@@ -229,6 +261,7 @@ __device__ __forceinline__ void down_wave(const DecodeKArgs &a, uint32_t wv, uin
             LaneRows<BS, ST, kDownFR> L;
             L.load(a.sd, rows, ok, cl, C);
             loads_issued();
+            staged_row(slot, a.sh_act, a.ff, (int)(threadIdx.x & 63), cl, X.xr);
             L.dot(X.xr, X.finish(nullptr, 0.f, 0, 0), part);
 #pragma unroll
             for (int f = 0; f < kDownFR; f++) acc_s[f] += part[f];
@@ -240,20 +273,22 @@ template <int BITS, int ST>
 __global__ __launch_bounds__(64 * kDownMaxWaves) void decode_down_kernel(DecodeKArgs a) {
     __shared__ float red_r[kDownMaxWaves][128];
     __shared__ float red_s[kDownMaxWaves][128];
+    extern __shared__ float4 dslot[];  // [waves][ff / 4] when a.down_slots
     const int lane = threadIdx.x & 63;
     const uint32_t wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const uint32_t lpr = a.lpr_f, rpi = 64u / lpr, sub = lane / lpr, cl = lane % lpr;
     const uint32_t rows_per_block = rpi * kDownFR;
     const uint32_t row0 = blockIdx.x * rows_per_block;
+    float4 *slot = a.down_slots ? dslot + wv * (a.ff / 4) : nullptr;
     // issued first: needed only after the LDS combine
     const float shared_gate = a.has_shared ? a.sh_gate[0] : 0.f;
     float acc_r[kDownFR], acc_s[kDownFR];
 #pragma unroll
     for (int f = 0; f < kDownFR; f++) acc_r[f] = acc_s[f] = 0.f;
     switch (a.has_shared ? a.sd.bits : BITS) {
-    case 2: down_wave<BITS, ST, 2>(a, wv, nw, row0, sub, cl, rpi, acc_r, acc_s); break;
-    case 4: down_wave<BITS, ST, 4>(a, wv, nw, row0, sub, cl, rpi, acc_r, acc_s); break;
-    default: down_wave<BITS, ST, 8>(a, wv, nw, row0, sub, cl, rpi, acc_r, acc_s); break;
+    case 2: down_wave<BITS, ST, 2>(a, wv, nw, row0, sub, cl, rpi, slot, acc_r, acc_s); break;
+    case 4: down_wave<BITS, ST, 4>(a, wv, nw, row0, sub, cl, rpi, slot, acc_r, acc_s); break;
+    default: down_wave<BITS, ST, 8>(a, wv, nw, row0, sub, cl, rpi, slot, acc_r, acc_s); break;
     }
     static_assert(kDownFR == 2, "reduce-scatter layout assumes two rows per sub-wave");
     if (lpr >= 16) {
@@ -340,8 +375,13 @@ static hipError_t launch_decode_t(Prof *p, hipStream_t s, const DecodeKArgs &k) 
     const uint32_t rows_per_block = (64u / k.lpr_f) * kDownFR;
     const uint32_t n_exp = k.k + (k.has_shared ? 1u : 0u);
     const uint32_t nw = n_exp < (uint32_t)kDownMaxWaves ? n_exp : (uint32_t)kDownMaxWaves;
+    // one activation-row slot per wave when they fit beside the combine arrays
+    DecodeKArgs kd = k;
+    const size_t slots = (size_t)nw * k.ff * 4;
+    kd.down_slots = slots <= kDownSlotBytes ? 1u : 0u;
     return launch_kernel(p, "decode_down", decode_down_kernel<BITS, ST>,
-                         dim3((k.h + rows_per_block - 1) / rows_per_block), dim3(64 * nw), 0, s, k);
+                         dim3((k.h + rows_per_block - 1) / rows_per_block), dim3(64 * nw),
+                         kd.down_slots ? slots : 0, s, kd);
 }
 
 hipError_t launch_decode(Prof *p, hipStream_t s, const DecodeArgs &a) {

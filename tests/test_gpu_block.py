@@ -220,6 +220,24 @@ def test_batched_decode_layouts(gpu, experts, T):
     assert rel_max_err(got[0], ref[0]) <= F32_TOL
 
 
+@pytest.mark.parametrize("shared", [0, 2048])
+def test_decode_long_down_rows(gpu, shared):
+    """Fused decode with 2048-wide down rows (ff 2048, K 8): the activation
+    slots of the down kernel's waves would exceed its LDS share, so each wave
+    loads its activation row directly."""
+    print(f"[case] decode ff 2048 shared={shared}", flush=True)
+    kinds = {"router": DENSE, "experts": (4, 64, BF16), "shared": (4, 64, BF16), "shared_gate": DENSE}
+    blk = HostBlock(256, 16, 8, 2048, shared, kinds, seed=90 + (shared > 0), random_experts=True)
+    bw = blk.upload(gpu)
+    for seed in range(2):
+        x = synth.normal(5100 + seed, 256).reshape(1, 256)
+        got = run_block(gpu, bw, x, 1, PATH_AUTO)
+        check_against_oracle(blk, x, got)
+        ref = run_block(gpu, bw, x, 1, PATH_GROUPED)
+        assert np.array_equal(got[2], ref[2])
+        assert rel_max_err(got[0], ref[0]) <= F32_TOL
+
+
 # ------------------------------------------------------------------ config 5 --
 @pytest.fixture(scope="module")
 def c5(gpu):
