@@ -147,13 +147,56 @@ __global__ __launch_bounds__(64) void seg_gateup_kernel(SegArgs a) {
                 });
 }
 
+// Same as over_inputs for rows that span fewer than 64 lanes (rpi > 1
+// sub-waves need the same chunk): each input row is loaded once per wave
+// (lane l: float4s l, l + 64, ...), written to one of the wave's two LDS
+// slots (float4 i of chunk c at i * C + c) and read back per sub-wave; the
+// next row's loads are in flight while the current row is multiplied.
+template <typename RowOf, typename Body>
+__device__ __forceinline__ void over_inputs_staged(float4 *slots, const float *in, uint32_t width,
+                                                   int lane, uint32_t cl, uint32_t beg, uint32_t end,
+                                                   RowOf row_of, Body body) {
+    constexpr int kMaxPerLane = 8;  // width <= 2048
+    const uint32_t C = width / 32, n4 = width / 4;
+    float4 nx[kMaxPerLane];
+    auto fetch = [&](uint32_t p) {
+        const float4 *src = reinterpret_cast<const float4 *>(in + (uint64_t)row_of(p) * width);
+#pragma unroll
+        for (int j = 0; j < kMaxPerLane; j++)
+            if ((uint32_t)(lane + 64 * j) < n4) nx[j] = src[lane + 64 * j];
+    };
+    fetch(beg);
+#pragma unroll 1
+    for (uint32_t p = beg; p < end; p++) {
+        float4 *slot = slots + (p & 1) * n4;
+#pragma unroll
+        for (int j = 0; j < kMaxPerLane; j++) {
+            const uint32_t w4 = lane + 64 * j;
+            if (w4 < n4) slot[(w4 % 8) * C + w4 / 8] = nx[j];
+        }
+        if (p + 1 < end) fetch(p + 1);
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's slot writes landed
+        __builtin_amdgcn_wave_barrier();
+        InChunk X;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 v = slot[i * C + cl];
+            X.v[4 * i] = v.x;
+            X.v[4 * i + 1] = v.y;
+            X.v[4 * i + 2] = v.z;
+            X.v[4 * i + 3] = v.w;
+        }
+        body(X, p);
+    }
+}
+
 // grid: x = row groups of kSegRowsFR * rpi rows, y = entries.
 template <int BITS, int ST, int LPR>
 __global__ __launch_bounds__(64) void seg_rows_kernel(SegArgs a) {
     const int lane = threadIdx.x;
     uint32_t e, beg, end;
     if (!seg_entry(a, blockIdx.y, e, beg, end)) return;
-    const uint32_t in = a.w.in, out = a.w.out;
+    const uint32_t in = LPR ? (uint32_t)LPR * 32u : a.w.in, out = a.w.out;
     const uint32_t lpr = lanes_per_row<LPR>(a.w), rpi = 64u / lpr, sub = lane / lpr, cl = lane % lpr;
     uint64_t rows[kSegRowsFR];
     bool ok[kSegRowsFR];
@@ -167,20 +210,26 @@ __global__ __launch_bounds__(64) void seg_rows_kernel(SegArgs a) {
     LaneRows<BITS, ST, kSegRowsFR> L;
     L.load(a.w, rows, ok, cl, lpr);
     loads_issued();
-    over_inputs(a.in, in, cl, beg, end, [](uint32_t p) { return p; },
-                [&](const InChunk &X, uint32_t p) {
-                    L.pin();  // convert the codes per input row: all rows' would not fit
-                    float res[kSegRowsFR];
-                    L.dot(X.v, X.sum(), res);
+    auto body = [&](const InChunk &X, uint32_t p) {
+        L.pin();  // convert the codes per input row: all rows' would not fit
+        float res[kSegRowsFR];
+        L.dot(X.v, X.sum(), res);
 #pragma unroll
-                    for (int f = 0; f < kSegRowsFR; f++) {
-                        const float v = subwave_sum(res[f], (int)lpr);
-                        if (cl == 0 && ok[f]) {
-                            const uint64_t o = (uint64_t)p * out + r[f];
-                            a.out[o] = a.bias ? v + a.bias[o] : v;
-                        }
-                    }
-                });
+        for (int f = 0; f < kSegRowsFR; f++) {
+            const float v = subwave_sum(res[f], (int)lpr);
+            if (cl == 0 && ok[f]) {
+                const uint64_t o = (uint64_t)p * out + r[f];
+                a.out[o] = a.bias ? v + a.bias[o] : v;
+            }
+        }
+    };
+    if (lpr < 64) {
+        // rows of fewer than 64 lanes: the input rows through the wave's LDS slots
+        extern __shared__ float4 slots[];  // 2 x in / 4
+        over_inputs_staged(slots, a.in, in, lane, cl, beg, end, [](uint32_t p) { return p; }, body);
+    } else {
+        over_inputs(a.in, in, cl, beg, end, [](uint32_t p) { return p; }, body);
+    }
 }
 
 // ------------------------------------------------------------------ host --
@@ -216,8 +265,10 @@ struct SegLaunch {
                                  dim3((a.w.out + per - 1) / per, entries), dim3(64), 0, s, a);
         } else {
             const uint32_t per = kSegRowsFR * rpi;
+            // two input-row slots per wave when rows span fewer than 64 lanes
+            const size_t lds = rpi > 1 ? 2 * (size_t)a.w.in * 4 : 0;
             return launch_kernel(p, name, seg_rows_kernel<BITS, T, LPR>,
-                                 dim3((a.w.out + per - 1) / per, entries), dim3(64), 0, s, a);
+                                 dim3((a.w.out + per - 1) / per, entries), dim3(64), lds, s, a);
         }
     }
     template <int BITS, int T>
