@@ -17,7 +17,6 @@ namespace moehip {
 struct DecodeKArgs {
     WDesc router, gate, up, down, sg, su, sd, sgi;
     uint32_t has_shared, k, normalize;
-    uint32_t down_slots;  // decode_down stages each wave's activation row in LDS
     uint32_t h, ff, ffs, E;
     uint32_t lpr_h, lpr_f;  // lanes per row along h / along ff (powers of two <= 64)
     uint32_t n_router_waves, n_shared_waves, n_gate_waves_per_expert;
@@ -197,9 +196,10 @@ constexpr size_t kDownSlotBytes = 48 * 1024;  // beside the 16 KiB combine array
 // so a sub-wave's 16 lanes read consecutive slots); the direct loads fetched
 // the row once per sub-wave (64 / lpr times).  Without a slot (rows too long
 // for the block's LDS), direct loads.
+template <bool SLOTS>
 __device__ __forceinline__ void staged_row(float4 *slot, const float *src, uint32_t ff, int lane,
                                            uint32_t cl, float *xr) {
-    if (!slot) {
+    if constexpr (!SLOTS) {
         XChunk X;
         X.load(src, nullptr, cl);
 #pragma unroll
@@ -221,7 +221,7 @@ __device__ __forceinline__ void staged_row(float4 *slot, const float *src, uint3
     }
 }
 
-template <int BITS, int ST, int BS>
+template <int BITS, int ST, int BS, bool SLOTS>
 __device__ __forceinline__ void down_wave(const DecodeKArgs &a, uint32_t wv, uint32_t nw,
                                           uint32_t row0, uint32_t sub, uint32_t cl, uint32_t rpi,
                                           float4 *slot, float *acc_r, float *acc_s) {
@@ -247,7 +247,7 @@ __device__ __forceinline__ void down_wave(const DecodeKArgs &a, uint32_t wv, uin
             LaneRows<BITS, ST, kDownFR> L;
             L.load(a.down, rows, ok, cl, C);
             loads_issued();
-            staged_row(slot, a.act + (uint64_t)kk * a.ff, a.ff, (int)(threadIdx.x & 63), cl, X.xr);
+            staged_row<SLOTS>(slot, a.act + (uint64_t)kk * a.ff, a.ff, (int)(threadIdx.x & 63), cl, X.xr);
             L.dot(X.xr, X.finish(nullptr, 0.f, 0, 0), part);
 #pragma unroll
             for (int f = 0; f < kDownFR; f++) acc_r[f] += part[f] * wk;
@@ -261,7 +261,7 @@ __device__ __forceinline__ void down_wave(const DecodeKArgs &a, uint32_t wv, uin
             LaneRows<BS, ST, kDownFR> L;
             L.load(a.sd, rows, ok, cl, C);
             loads_issued();
-            staged_row(slot, a.sh_act, a.ff, (int)(threadIdx.x & 63), cl, X.xr);
+            staged_row<SLOTS>(slot, a.sh_act, a.ff, (int)(threadIdx.x & 63), cl, X.xr);
             L.dot(X.xr, X.finish(nullptr, 0.f, 0, 0), part);
 #pragma unroll
             for (int f = 0; f < kDownFR; f++) acc_s[f] += part[f];
@@ -269,26 +269,26 @@ __device__ __forceinline__ void down_wave(const DecodeKArgs &a, uint32_t wv, uin
     }
 }
 
-template <int BITS, int ST>
+template <int BITS, int ST, bool SLOTS>
 __global__ __launch_bounds__(64 * kDownMaxWaves) void decode_down_kernel(DecodeKArgs a) {
     __shared__ float red_r[kDownMaxWaves][128];
     __shared__ float red_s[kDownMaxWaves][128];
-    extern __shared__ float4 dslot[];  // [waves][ff / 4] when a.down_slots
+    extern __shared__ float4 dslot[];  // [waves][ff / 4] with SLOTS
     const int lane = threadIdx.x & 63;
     const uint32_t wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const uint32_t lpr = a.lpr_f, rpi = 64u / lpr, sub = lane / lpr, cl = lane % lpr;
     const uint32_t rows_per_block = rpi * kDownFR;
     const uint32_t row0 = blockIdx.x * rows_per_block;
-    float4 *slot = a.down_slots ? dslot + wv * (a.ff / 4) : nullptr;
+    float4 *slot = SLOTS ? dslot + wv * (a.ff / 4) : nullptr;
     // issued first: needed only after the LDS combine
     const float shared_gate = a.has_shared ? a.sh_gate[0] : 0.f;
     float acc_r[kDownFR], acc_s[kDownFR];
 #pragma unroll
     for (int f = 0; f < kDownFR; f++) acc_r[f] = acc_s[f] = 0.f;
     switch (a.has_shared ? a.sd.bits : BITS) {
-    case 2: down_wave<BITS, ST, 2>(a, wv, nw, row0, sub, cl, rpi, slot, acc_r, acc_s); break;
-    case 4: down_wave<BITS, ST, 4>(a, wv, nw, row0, sub, cl, rpi, slot, acc_r, acc_s); break;
-    default: down_wave<BITS, ST, 8>(a, wv, nw, row0, sub, cl, rpi, slot, acc_r, acc_s); break;
+    case 2: down_wave<BITS, ST, 2, SLOTS>(a, wv, nw, row0, sub, cl, rpi, slot, acc_r, acc_s); break;
+    case 4: down_wave<BITS, ST, 4, SLOTS>(a, wv, nw, row0, sub, cl, rpi, slot, acc_r, acc_s); break;
+    default: down_wave<BITS, ST, 8, SLOTS>(a, wv, nw, row0, sub, cl, rpi, slot, acc_r, acc_s); break;
     }
     static_assert(kDownFR == 2, "reduce-scatter layout assumes two rows per sub-wave");
     if (lpr >= 16) {
@@ -376,12 +376,11 @@ static hipError_t launch_decode_t(Prof *p, hipStream_t s, const DecodeKArgs &k) 
     const uint32_t n_exp = k.k + (k.has_shared ? 1u : 0u);
     const uint32_t nw = n_exp < (uint32_t)kDownMaxWaves ? n_exp : (uint32_t)kDownMaxWaves;
     // one activation-row slot per wave when they fit beside the combine arrays
-    DecodeKArgs kd = k;
     const size_t slots = (size_t)nw * k.ff * 4;
-    kd.down_slots = slots <= kDownSlotBytes ? 1u : 0u;
-    return launch_kernel(p, "decode_down", decode_down_kernel<BITS, ST>,
-                         dim3((k.h + rows_per_block - 1) / rows_per_block), dim3(64 * nw),
-                         kd.down_slots ? slots : 0, s, kd);
+    const dim3 grid((k.h + rows_per_block - 1) / rows_per_block), block(64 * nw);
+    if (slots <= kDownSlotBytes)
+        return launch_kernel(p, "decode_down", decode_down_kernel<BITS, ST, true>, grid, block, slots, s, k);
+    return launch_kernel(p, "decode_down", decode_down_kernel<BITS, ST, false>, grid, block, 0, s, k);
 }
 
 hipError_t launch_decode(Prof *p, hipStream_t s, const DecodeArgs &a) {
