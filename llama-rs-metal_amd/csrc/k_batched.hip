@@ -223,8 +223,9 @@ __global__ __launch_bounds__(64) void seg_rows_kernel(SegArgs a) {
             }
         }
     };
-    if (lpr < 64) {
-        // rows of fewer than 64 lanes: the input rows through the wave's LDS slots
+    if constexpr (LPR != 64) {
+        // rows of fewer than 64 lanes (the run-time width is never 64: those
+        // rows take LPR 64): the input rows through the wave's LDS slots
         extern __shared__ float4 slots[];  // 2 x in / 4
         over_inputs_staged(slots, a.in, in, lane, cl, beg, end, [](uint32_t p) { return p; }, body);
     } else {
@@ -266,7 +267,7 @@ struct SegLaunch {
         } else {
             const uint32_t per = kSegRowsFR * rpi;
             // two input-row slots per wave when rows span fewer than 64 lanes
-            const size_t lds = rpi > 1 ? 2 * (size_t)a.w.in * 4 : 0;
+            const size_t lds = LPR != 64 ? 2 * (size_t)a.w.in * 4 : 0;
             return launch_kernel(p, name, seg_rows_kernel<BITS, T, LPR>,
                                  dim3((a.w.out + per - 1) / per, entries), dim3(64), lds, s, a);
         }
