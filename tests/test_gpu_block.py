@@ -238,6 +238,27 @@ def test_decode_long_down_rows(gpu, shared):
         assert rel_max_err(got[0], ref[0]) <= F32_TOL
 
 
+@pytest.mark.parametrize("E,K,normalize,ffs", [(64, 1, True, 128), (32, 32, False, 0), (100, 7, False, 128)])
+@pytest.mark.parametrize("T", [1, 5, 300])
+def test_routing_edges_every_path(gpu, E, K, normalize, ffs, T):
+    """Top-1, top-E (every expert selected), an expert count that is no power
+    of two, and unnormalised routing weights, through the fused decode (T 1),
+    the batched decode (T 5) and the bf16-MFMA path (T 300)."""
+    print(f"[case] routing edges E={E} K={K} normalize={normalize} ffs={ffs} T={T}", flush=True)
+    kinds = {"router": DENSE, "experts": (4, 64, BF16), "shared": (4, 64, BF16), "shared_gate": DENSE}
+    blk = HostBlock(256, E, K, 128, ffs, kinds, seed=E + K, normalize=normalize, random_experts=True)
+    bw = blk.upload(gpu)
+    x = synth.normal(5200 + E + T, T * 256).reshape(T, 256)
+    got = run_block(gpu, bw, x, T, PATH_AUTO)
+    if T == 300:
+        check_against_oracle(blk, x, got, tokens=range(0, T, 13), tol=BF16_TOL, logit_tol=BF16_TOL)
+    else:
+        check_against_oracle(blk, x, got)
+        ref = run_block(gpu, bw, x, T, PATH_GROUPED)
+        assert np.array_equal(got[2], ref[2])
+        assert rel_max_err(got[0], ref[0]) <= F32_TOL
+
+
 # ------------------------------------------------------------------ config 5 --
 @pytest.fixture(scope="module")
 def c5(gpu):
