@@ -43,6 +43,10 @@ struct Alloc {
 struct moe_gpu {
     int device = 0;
     hipStream_t stream = nullptr;
+    // second stream for work independent of the routing (the shared expert),
+    // forked from and joined back into `stream` with these events
+    hipStream_t side = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     std::map<uintptr_t, Alloc> allocs;
     uint64_t live = 0;
     bool in_batch = false;

@@ -69,7 +69,10 @@ moe_status moe_gpu_create(int device, moe_gpu **out) {
     g->device = device;
     g->name = prop.name;
     if (hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking) != hipSuccess ||
-        hipEventCreate(&g->ev_begin) != hipSuccess || hipEventCreate(&g->ev_end) != hipSuccess) {
+        hipStreamCreateWithFlags(&g->side, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreate(&g->ev_begin) != hipSuccess || hipEventCreate(&g->ev_end) != hipSuccess ||
+        hipEventCreateWithFlags(&g->ev_fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&g->ev_join, hipEventDisableTiming) != hipSuccess) {
         delete g;
         return MOE_ERR_GPU;
     }
@@ -88,8 +91,12 @@ void moe_gpu_destroy(moe_gpu *g) {
         (void)hipEventDestroy(q.b);
     }
     for (auto e : g->prof.pool) (void)hipEventDestroy(e);
+    (void)hipStreamSynchronize(g->side);
     (void)hipEventDestroy(g->ev_begin);
     (void)hipEventDestroy(g->ev_end);
+    (void)hipEventDestroy(g->ev_fork);
+    (void)hipEventDestroy(g->ev_join);
+    (void)hipStreamDestroy(g->side);
     (void)hipStreamDestroy(g->stream);
     delete g;
 }

@@ -242,6 +242,24 @@ moe_status run_batched(moe_gpu *g, const moe_block_weights *w, const Dims &d, co
     float *act = ws + L.act, *yexp = ws + L.yexp;
     const uint32_t runs = seg_max_entries(t32, 0), entries = seg_max_entries(t32 * K, E);
     const float *bias = has(io->logit_bias) ? fp(io->logit_bias) : nullptr;
+    // the shared expert needs only the input: it runs on the side stream,
+    // concurrently with the routed chain, and joins before the combine
+    const float *so = nullptr, *sgv = nullptr;
+    if (w->has_shared) {
+        float *sh = ws + L.sh_act, *sout = ws + L.sh_out, *sgt = ws + L.sh_gate;
+        hipStream_t ss = g->side;
+        TRY(hipEventRecord(g->ev_fork, s));
+        TRY(hipStreamWaitEvent(ss, g->ev_fork, 0));
+        TRY(launch_seg_gateup(p, ss, "seg_shared_gateup", wdesc(w->shared_gate), wdesc(w->shared_up), xin,
+                              nullptr, 1, nullptr, nullptr, nullptr, t32, runs, sh));
+        TRY(launch_seg_rows(p, ss, "seg_shared_down", wdesc(w->shared_down), sh, nullptr, nullptr, nullptr,
+                            t32, runs, nullptr, sout));
+        TRY(launch_seg_rows(p, ss, "seg_shared_gate", gate_inp_desc(w->shared_gate_inp), xin, nullptr,
+                            nullptr, nullptr, t32, runs, nullptr, sgt));
+        TRY(hipEventRecord(g->ev_join, ss));
+        so = sout;
+        sgv = sgt;
+    }
     TRY(launch_seg_rows(p, s, "seg_router", wdesc(w->router), xin, nullptr, nullptr, nullptr, t32, runs,
                         bias, logits));
     TRY(launch_route(p, s, logits, E, K, w->normalize ? 1 : 0, t32, ids, wts));
@@ -251,18 +269,7 @@ moe_status run_batched(moe_gpu *g, const moe_block_weights *w, const Dims &d, co
                           offsets, 0, entries, act));
     TRY(launch_seg_rows(p, s, "seg_down", wdesc(w->down), act, tiles, ntiles, offsets, 0, entries,
                         nullptr, yexp));
-    const float *so = nullptr, *sgv = nullptr;
-    if (w->has_shared) {
-        float *sh = ws + L.sh_act, *sout = ws + L.sh_out, *sgt = ws + L.sh_gate;
-        TRY(launch_seg_gateup(p, s, "seg_shared_gateup", wdesc(w->shared_gate), wdesc(w->shared_up), xin,
-                              nullptr, 1, nullptr, nullptr, nullptr, t32, runs, sh));
-        TRY(launch_seg_rows(p, s, "seg_shared_down", wdesc(w->shared_down), sh, nullptr, nullptr, nullptr,
-                            t32, runs, nullptr, sout));
-        TRY(launch_seg_rows(p, s, "seg_shared_gate", gate_inp_desc(w->shared_gate_inp), xin, nullptr,
-                            nullptr, nullptr, t32, runs, nullptr, sgt));
-        so = sout;
-        sgv = sgt;
-    }
+    if (w->has_shared) TRY(hipStreamWaitEvent(s, g->ev_join, 0));
     TRY(launch_combine(p, s, yexp, pos, wts, K, so, sgv, io->residual ? xres : nullptr, out, t32,
                        (uint32_t)d.h));
     return MOE_OK;
@@ -314,20 +321,26 @@ moe_status run_mfma(moe_gpu *g, const moe_block_weights *w, const Dims &d, const
         TRY(launch_route(p, s, logits, E, K, w->normalize ? 1 : 0, (uint32_t)T, ids, wts));
     }
     TRY(launch_dispatch(p, s, ids, (uint32_t)(T * K), E, counts, offsets, perm, pos));
-    TRY(launch_mfma_experts(p, s, wdesc(w->gate), wdesc(w->up), wdesc(w->down), packed(w->gate_packed),
-                            packed(w->up_packed), packed(w->down_packed), xb16, (uint32_t)T, offsets, perm,
-                            K, tiles, ntiles, act16, y16));
+    // the shared expert needs only the input: side stream, joined before the combine
     const float *so = nullptr, *sgv = nullptr;
     if (w->has_shared) {
         float *sg = ws + L.sh_act, *su = ws + L.sh_up, *sout = ws + L.sh_out, *sgt = ws + L.sh_gate;
-        TRY(launch_gemv(p, s, wdesc(w->shared_gate), xin, 0, nullptr, 1, sg, (uint32_t)T));
-        TRY(launch_gemv(p, s, wdesc(w->shared_up), xin, 0, nullptr, 1, su, (uint32_t)T));
-        TRY(launch_swiglu(p, s, sg, su, sg, T * d.ffs));
-        TRY(launch_gemv(p, s, wdesc(w->shared_down), sg, 0, nullptr, 1, sout, (uint32_t)T));
-        TRY(launch_gemv(p, s, gate_inp_desc(w->shared_gate_inp), xin, 0, nullptr, 1, sgt, (uint32_t)T));
+        hipStream_t ss = g->side;
+        TRY(hipEventRecord(g->ev_fork, s));
+        TRY(hipStreamWaitEvent(ss, g->ev_fork, 0));
+        TRY(launch_gemv(p, ss, wdesc(w->shared_gate), xin, 0, nullptr, 1, sg, (uint32_t)T));
+        TRY(launch_gemv(p, ss, wdesc(w->shared_up), xin, 0, nullptr, 1, su, (uint32_t)T));
+        TRY(launch_swiglu(p, ss, sg, su, sg, T * d.ffs));
+        TRY(launch_gemv(p, ss, wdesc(w->shared_down), sg, 0, nullptr, 1, sout, (uint32_t)T));
+        TRY(launch_gemv(p, ss, gate_inp_desc(w->shared_gate_inp), xin, 0, nullptr, 1, sgt, (uint32_t)T));
+        TRY(hipEventRecord(g->ev_join, ss));
         so = sout;
         sgv = sgt;
     }
+    TRY(launch_mfma_experts(p, s, wdesc(w->gate), wdesc(w->up), wdesc(w->down), packed(w->gate_packed),
+                            packed(w->up_packed), packed(w->down_packed), xb16, (uint32_t)T, offsets, perm,
+                            K, tiles, ntiles, act16, y16));
+    if (w->has_shared) TRY(hipStreamWaitEvent(s, g->ev_join, 0));
     TRY(launch_combine16(p, s, y16, pos, wts, K, so, sgv, io->residual ? xraw : nullptr, out, (uint32_t)T,
                          (uint32_t)d.h));
     return MOE_OK;

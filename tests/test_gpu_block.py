@@ -259,6 +259,32 @@ def test_routing_edges_every_path(gpu, E, K, normalize, ffs, T):
         assert rel_max_err(got[0], ref[0]) <= F32_TOL
 
 
+def test_config3_batched_graph_replay(gpu, c3):
+    """The batched decode with its shared expert forked onto the side stream,
+    captured into a graph and replayed (eager work between replays): every
+    replay equals the eager result bit for bit."""
+    blk, bw = c3
+    T = 8
+    x = synth.normal(2100, T * 2048)
+    bias = hot_bias(T, 512, seed=21)
+    eager = run_block(gpu, bw, x.reshape(T, -1), T, PATH_AUTO, bias=bias)[0].ravel()
+    xb, bb = gpu.upload(x), gpu.upload(bias)
+    out = gpu.zeros(T * 2048)
+    ws = gpu.zeros(bw.workspace_elems(T))
+    cap = gpu.capture()
+    with cap as b:
+        b.moe_block(bw, xb, out, T, ws, logit_bias=bb)
+    for i in range(3):
+        gpu.clear(out)
+        with gpu.batch() as b:
+            b.graph(cap.graph)
+        assert np.array_equal(gpu.read(out), eager), i
+        run_block(gpu, bw, synth.normal(2200 + i, T * 2048).reshape(T, -1), T, PATH_AUTO,
+                  bias=hot_bias(T, 512, seed=30 + i))
+    for buf in (xb, bb, out, ws):
+        gpu.release(buf)
+
+
 # ------------------------------------------------------------------ config 5 --
 @pytest.fixture(scope="module")
 def c5(gpu):
