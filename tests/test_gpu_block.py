@@ -13,7 +13,8 @@ import oracle
 from helpers import (DENSE, HostBlock, close, config1, config2, config3, config4, config5, hot_bias,
                      pack_reference, rel_max_err, zipf_bias)
 from hip_backend import (BF16, F16, F32, PATH_AUTO, PATH_GROUPED, PATH_MFMA, PATH_OPS, BlockWeights,
-                         Tensor, synth)
+                         ShapeError, Tensor, synth)
+from hip_backend.api import MoePackedWeightC, MoeRegionC, PackedWeight
 
 pytestmark = pytest.mark.gpu
 
@@ -450,6 +451,48 @@ def test_pack_weight_layout(gpu, dims, bits, group, st):
     assert np.array_equal(gpu.read(pw.buffers[0]).view(np.uint32), codes)
     assert np.array_equal(gpu.read(pw.buffers[1]).view(np.uint16), scales)
     assert np.array_equal(gpu.read(pw.buffers[2]).view(np.uint16), biases)
+
+
+def test_packed_weights_are_validated(gpu):
+    """moe_pack_weight and moe_block refuse packed copies that do not fit:
+    wrong region sizes, an output overlapping the weight, a gate copy without
+    the up copy, and weights without a packed form (F32 scales)."""
+    def tensor(dims, st, seed):
+        return Tensor.affine(dims, *synth.random_affine(seed, int(np.prod(dims)), 4, 64, st), 4, 64, st)
+
+    gate = gpu.weight_tensor(tensor([256, 128, 4], BF16, 1))
+    up = gpu.weight_tensor(tensor([256, 128, 4], BF16, 2))
+    down = gpu.weight_tensor(tensor([128, 256, 4], BF16, 3))
+    router = gpu.weight_f32(synth.normal(4, 256 * 4), [256, 4])
+    pg, pu = gpu.pack_weight(gate), gpu.pack_weight(up)
+    # a region one element short
+    c = MoePackedWeightC.from_buffer_copy(pg.c)
+    c.data.bytes -= 4
+    with pytest.raises(ShapeError):
+        with gpu.batch() as b:
+            b.pack_weight(gate, PackedWeight(c, pg.buffers))
+    # the copy written over the weight itself
+    c = MoePackedWeightC.from_buffer_copy(pg.c)
+    c.data = MoeRegionC(gate.c.data.ptr, c.data.bytes)
+    with pytest.raises(ShapeError):
+        with gpu.batch() as b:
+            b.pack_weight(gate, PackedWeight(c, pg.buffers))
+    # gate copy without the up copy, and a down copy one element short in the block
+    x = gpu.upload(synth.normal(5, 300 * 256))
+    out = gpu.zeros(300 * 256)
+    pd = gpu.pack_weight(down)
+    c = MoePackedWeightC.from_buffer_copy(pd.c)
+    c.scales.bytes -= 4
+    for packed in ([pg, None, None], [pg, pu, PackedWeight(c, pd.buffers)]):
+        bwp = BlockWeights(router, gate, up, down, 2, True, packed=packed)
+        ws = gpu.zeros(bwp.workspace_elems(300))
+        with pytest.raises(ShapeError):
+            with gpu.batch() as b:
+                b.moe_block(bwp, x, out, 300, ws, path=PATH_MFMA)
+        gpu.release(ws)
+    # F32 scales have no packed form
+    f32s = gpu.weight_tensor(tensor([256, 128, 4], F32, 6))
+    assert gpu.pack_weight(f32s) is None
 
 
 @pytest.mark.parametrize("bits,group,st", [(2, 32, BF16), (4, 64, F16), (4, 128, BF16), (8, 64, BF16),
