@@ -13,7 +13,8 @@
 //           one segment of all tokens, its K split into ksplit ranges whose
 //           F32 partial sums the routing kernel adds in range order
 //
-// Work item = kTM pairs of one expert x one 128-row N-tile over the full K
+// Work item = kTM pairs of one expert x one N-tile (128 weight rows for
+// grouped_gemm, 64 per wave for affine_gemm) over the full K
 // (ROUTER: over one of its K ranges).
 // Blocks are persistent: the items are split into eight contiguous ranges,
 // one per XCD (workgroup b runs on XCD b % 8), and the blocks of an XCD walk
@@ -22,12 +23,13 @@
 //
 // Two kernels share that schedule.  affine_gemm_kernel (GATEUP and DOWN over
 // 2/4/8-bit affine weights, the prefill hot path) keeps the weights out of
-// LDS: each of its two waves owns all kTM rows and 64 weight rows of the
+// LDS: each of its four waves owns all kTM rows and 64 weight rows of the
 // tile, loads its own codes into registers and dequantises them straight
 // into MFMA operands (every weight value once per block), while the A tile
 // reaches LDS by buffer DMA (buffer_load_dwordx4 ... lds), 16-byte chunks
-// XOR-swizzled so the fragment reads are conflict-free.  Four such blocks
-// share a CU.  grouped_gemm_kernel (ROUTER, dense weights, and tensors whose
+// XOR-swizzled so the fragment reads are conflict-free.  Two such blocks
+// share a CU; the four waves share one A stage, so per multiply-add half the
+// A bytes of two-wave blocks move into the CU.  grouped_gemm_kernel (ROUTER, dense weights, and tensors whose
 // offsets exceed 32 bits) stages both operands through LDS:
 //
 // Per 64-wide K step, double-buffered in LDS: the block's threads load the
@@ -424,8 +426,9 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void grouped_gemm_kernel(Ar
 }
 
 // ------------------------------------------------------ affine_gemm ----
-constexpr int kAfThreads = 128;     // two waves
-constexpr int kAfBlocksPerCu = 4;   // 4 x 32 KiB of LDS, 2 waves per SIMD
+constexpr int kAfWaves = 4;                  // waves per block, sharing one A stage
+constexpr int kAfThreads = 64 * kAfWaves;
+constexpr int kAfBlocksPerCu = 2;            // 2 x 32 KiB of LDS, 2 waves per SIMD
 constexpr int kAfNT = 2;            // 32-row weight tiles per wave
 constexpr int kAfATile = kTM * kTK * 2;  // one A stage: kTM rows x 128 bytes
 
@@ -476,15 +479,16 @@ __device__ __forceinline__ void affine_item(const Args &a, uint8_t *abuf, uint32
     static_assert(!PK || GS != 0, "packed copies carry 16-bit scales");
     const int h = lane >> 5, l32 = lane & 31;
     const uint32_t in = a.w.in, out = a.w.out, nk = in / kTK;
-    constexpr int ND = 2 * NS;  // DMA instructions per wave and step (8 rows each)
-    // A: DMA instruction i of wave wv fills tile rows 16i + 8wv .. +7, lane
+    static_assert((4 * NS) % kAfWaves == 0, "the live rows split evenly over the waves' DMA");
+    constexpr int ND = 4 * NS / kAfWaves;  // DMA instructions per wave and step (8 rows each)
+    // A: DMA instruction i of wave wv fills tile rows 8 kAfWaves i + 8wv .. +7, lane
     // (row, chunk position) = (lane / 8, lane % 8); byte offsets below 2^32
     // (checked on the host).  Rows past the segment re-read its first row.
     const uint32_t drow = 8 * wv + (lane >> 3), dpos = lane & 7;
     uint32_t aoff[ND];
 #pragma unroll
     for (int i = 0; i < ND; i++) {
-        const uint32_t r = 16 * i + drow;
+        const uint32_t r = 8 * kAfWaves * i + drow;
         uint32_t pos = m0 + r;
         if (pos >= seg_end) pos = m0;
         const uint32_t src = MODE == GATEUP ? a.perm[pos] / a.k : pos;
@@ -499,7 +503,7 @@ __device__ __forceinline__ void affine_item(const Args &a, uint8_t *abuf, uint32
     const uint32_t ntile = (out + 31) / 32;
 #pragma unroll
     for (int t = 0; t < kAfNT; t++) {
-        uint32_t n = MODE == GATEUP ? nt * (kTN / 2) + 32 * wv + l32 : nt * kTN + 64 * wv + 32 * t + l32;
+        uint32_t n = MODE == GATEUP ? nt * (32 * kAfWaves) + 32 * wv + l32 : nt * (64 * kAfWaves) + 64 * wv + 32 * t + l32;
         const uint32_t tile = (e * ntile + n / 32);
         pko[t] = tile * nk * (256 * BITS) + lane * (4 * BITS);
         pks[t] = tile * (nk / 2) * (32 * kG2 * 2) + l32 * (kG2 * 2);
@@ -535,7 +539,7 @@ __device__ __forceinline__ void affine_item(const Args &a, uint8_t *abuf, uint32
         uint8_t *dst = abuf + buf * kAfATile + 8 * wv * (kTK * 2);
 #pragma unroll
         for (int i = 0; i < ND; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(dst + 16 * i * (kTK * 2)), 16, aoff[i],
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(dst + 8 * kAfWaves * i * (kTK * 2)), 16, aoff[i],
                                                      kb * (kTK * 2), 0, 0);
     };
     auto load_b = [&](AfStage<BITS> &st, uint32_t kb) {
@@ -685,7 +689,7 @@ __device__ __forceinline__ void affine_item(const Args &a, uint8_t *abuf, uint32
             const uint32_t pos = m0 + 32 * s + 8 * (r >> 2) + 4 * h + (r & 3);
             if (pos >= seg_end) continue;
             if constexpr (MODE == GATEUP) {
-                const uint32_t j = nt * (kTN / 2) + 32 * wv + l32;
+                const uint32_t j = nt * (32 * kAfWaves) + 32 * wv + l32;
                 if (j < out) {
                     // activation (elementwise.metal:8-17), base-2 exponential and
                     // hardware reciprocal; the result is rounded to bf16
@@ -696,7 +700,7 @@ __device__ __forceinline__ void affine_item(const Args &a, uint8_t *abuf, uint32
             } else {
 #pragma unroll
                 for (int t = 0; t < kAfNT; t++) {
-                    const uint32_t n = nt * kTN + 64 * wv + 32 * t + l32;
+                    const uint32_t n = nt * (64 * kAfWaves) + 64 * wv + 32 * t + l32;
                     if (n < out) a.out[(uint64_t)pos * out + n] = (uint16_t)(pack_bf16(acc[s][t][r], 0.f) & 0xffffu);
                 }
             }
@@ -715,8 +719,8 @@ __device__ __forceinline__ void affine_live(const Args &a, uint8_t *abuf, uint32
 }
 
 // Affine GATEUP / DOWN products: same persistent XCD-range schedule as
-// grouped_gemm_kernel, two waves per block, at most 256 VGPRs per lane so two
-// waves share a SIMD.
+// grouped_gemm_kernel, kAfWaves waves per block, at most 256 VGPRs per lane so
+// two waves share a SIMD.
 template <int MODE, int BITS, int T>
 __global__ __attribute__((amdgpu_flat_work_group_size(kAfThreads, kAfThreads), amdgpu_waves_per_eu(2, 2)))
 void affine_gemm_kernel(Args a) {
@@ -831,11 +835,11 @@ hipError_t launch_grouped_gemm(Prof *p, hipStream_t s, int down, const WDesc &w,
     }
     hipError_t e;
     if (down) {
-        a.n_tiles_n = (w.out + gemm::kTN - 1) / gemm::kTN;
+        a.n_tiles_n = affine ? (w.out + 64 * gemm::kAfWaves - 1) / (64 * gemm::kAfWaves) : (w.out + gemm::kTN - 1) / gemm::kTN;
         if (!affine && (e = dispatch_kind(w, SetLds<gemm::DOWN>{})) != hipSuccess) return e;
         e = dispatch_kind(w, gemm::Launch<gemm::DOWN>{p, s, a, blocks, affine, affine_blocks});
     } else {
-        a.n_tiles_n = (w.out + gemm::kTN / 2 - 1) / (gemm::kTN / 2);
+        a.n_tiles_n = affine ? (w.out + 32 * gemm::kAfWaves - 1) / (32 * gemm::kAfWaves) : (w.out + gemm::kTN / 2 - 1) / (gemm::kTN / 2);
         if (!affine && (e = dispatch_kind(w, SetLds<gemm::GATEUP>{})) != hipSuccess) return e;
         e = dispatch_kind(w, gemm::Launch<gemm::GATEUP>{p, s, a, blocks, affine, affine_blocks});
     }
