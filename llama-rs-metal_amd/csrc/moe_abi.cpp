@@ -67,7 +67,7 @@ moe_status moe_gpu_create(int device, moe_gpu **out) {
     if (hipSetDevice(device) != hipSuccess) return MOE_ERR_UNAVAILABLE;
     moe_gpu *g = new moe_gpu();
     g->device = device;
-    g->name = prop.name;
+    g->name = prop.name[0] ? prop.name : prop.gcnArchName;
     if (hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking) != hipSuccess ||
         hipStreamCreateWithFlags(&g->side, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreate(&g->ev_begin) != hipSuccess || hipEventCreate(&g->ev_end) != hipSuccess ||
