@@ -47,6 +47,8 @@ struct moe_gpu {
     // forked from and joined back into `stream` with these events
     hipStream_t side = nullptr;
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+    // device word of the fused route + dispatch launch: zero between launches
+    uint32_t *arrive = nullptr;
     std::map<uintptr_t, Alloc> allocs;
     uint64_t live = 0;
     bool in_batch = false;

@@ -286,4 +286,149 @@ hipError_t launch_dispatch(Prof *p, hipStream_t s, const uint32_t *ids, uint32_t
                          dim3(kDispThreads), 0, s, ids, pairs, experts, counts, offsets, perm, pos);
 }
 
+// ------------------------------------------------- route + dispatch, fused --
+// Routing of the T tokens (one wave per token, kRdWaves tokens per block), and
+// in the block that finishes last the dispatch of all T*K pairs and the
+// schedule of tm-pair work items (what dispatch_kernel and
+// tile_schedule_kernel produce, in one launch instead of three).  Every block
+// publishes its ids with a device-scope release and counts itself on
+// `arrive`; the block whose increment completes the count reads all ids after
+// an acquire and returns the counter to zero for the next launch.  No block
+// waits for another.  Pair placement is stable: wave w takes a contiguous
+// span of pairs, ranks inside a 64-pair round come from ballots over the
+// expert id bits, per-wave running counts carry them across rounds, and a
+// prefix over the waves orders the spans.
+constexpr int kRdWaves = 4;
+constexpr int kRdThreads = kRdWaves * 64;
+
+__global__ __launch_bounds__(kRdThreads) void route_dispatch_kernel(
+    const float *__restrict__ logits, uint32_t T, uint32_t E, uint32_t K, int normalize,
+    uint32_t *ids, float *__restrict__ weights, uint32_t *arrive, uint32_t tm,
+    uint32_t *__restrict__ counts, uint32_t *__restrict__ offsets, uint32_t *__restrict__ perm,
+    uint32_t *__restrict__ pos, uint32_t *__restrict__ tiles, uint32_t *__restrict__ ntiles) {
+    extern __shared__ uint32_t cw[];  // [kRdWaves][E]: per-wave expert counts, then bases
+    __shared__ RouteLds L[kRdWaves];
+    __shared__ uint32_t wsum[2][kRdWaves];
+    __shared__ uint32_t last;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const uint32_t t = blockIdx.x * kRdWaves + wv;
+    if (t < T)
+        route_one_wave(&L[wv], nullptr, logits + (uint64_t)t * E, E, K, normalize,
+                       ids + (uint64_t)t * K, weights + (uint64_t)t * K, lane);
+    __threadfence();
+    __syncthreads();
+    if (tid == 0)
+        last = __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
+               gridDim.x - 1;
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    if (tid == 0) __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    const uint32_t pairs = T * K;
+    const uint32_t span = (pairs + kRdThreads - 1) / kRdThreads * 64;
+    const uint32_t p0 = min(pairs, wv * span), p1 = min(pairs, p0 + span);
+    for (uint32_t i = tid; i < kRdWaves * E; i += kRdThreads) cw[i] = 0u;
+    __syncthreads();
+    for (uint32_t q = p0 + lane; q < p1; q += 64) {
+        const uint32_t e = ids[q];
+        if (e < E) atomicAdd(&cw[wv * E + e], 1u);
+    }
+    __syncthreads();
+    // scan over experts (thread tid owns [e0, e1)) of pair and work-item counts
+    const uint32_t per = (E + kRdThreads - 1) / kRdThreads;
+    const uint32_t e0 = min(E, (uint32_t)tid * per), e1 = min(E, e0 + per);
+    uint32_t part = 0, tpart = 0;
+    for (uint32_t e = e0; e < e1; e++) {
+        uint32_t c = 0;
+        for (int w = 0; w < kRdWaves; w++) c += cw[w * E + e];
+        part += c;
+        tpart += (c + tm - 1) / tm;
+    }
+    uint32_t incl = part, tincl = tpart;
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t v = __shfl_up(incl, o, 64), tv = __shfl_up(tincl, o, 64);
+        if (lane >= o) {
+            incl += v;
+            tincl += tv;
+        }
+    }
+    if (lane == 63) {
+        wsum[0][wv] = incl;
+        wsum[1][wv] = tincl;
+    }
+    __syncthreads();
+    uint32_t run = incl - part, trun = tincl - tpart, total = 0, ttotal = 0;
+    for (int w = 0; w < kRdWaves; w++) {
+        if (w < wv) {
+            run += wsum[0][w];
+            trun += wsum[1][w];
+        }
+        total += wsum[0][w];
+        ttotal += wsum[1][w];
+    }
+    for (uint32_t e = e0; e < e1; e++) {
+        uint32_t c = 0;
+        for (int w = 0; w < kRdWaves; w++) {
+            const uint32_t v = cw[w * E + e];
+            cw[w * E + e] = run + c;
+            c += v;
+        }
+        counts[e] = c;
+        offsets[e] = run;
+        const uint32_t nt = (c + tm - 1) / tm;
+        for (uint32_t i = 0; i < nt; i++) {
+            tiles[2 * (trun + i)] = e;
+            tiles[2 * (trun + i) + 1] = run + i * tm;
+        }
+        trun += nt;
+        run += c;
+    }
+    if (tid == 0) {
+        offsets[E] = total;
+        *ntiles = ttotal;
+    }
+    __syncthreads();
+    const int bits = 32 - __clz((int)E);  // distinguishes 0..E (E marks an absent pair)
+    const uint64_t below = (1ull << lane) - 1ull;
+    for (uint32_t b = p0; b < p1; b += 64) {
+        const uint32_t q = b + lane;
+        uint32_t e = q < p1 ? ids[q] : E;
+        if (e > E) e = E;
+        uint64_t same = ~0ull;
+        for (int i = 0; i < bits; i++) {
+            const bool bit = (e >> i) & 1u;
+            const uint64_t m = __ballot(bit);
+            same &= bit ? m : ~m;
+        }
+        const uint32_t c = e < E ? cw[wv * E + e] : 0u;
+        // the group's last lane advances the running base (the wave's LDS
+        // operations execute in order, so every lane read the old value)
+        if (e < E && (same >> lane) == 1ull) cw[wv * E + e] = c + (uint32_t)__popcll(same);
+        if (e < E) {
+            const uint32_t at = c + (uint32_t)__popcll(same & below);
+            perm[at] = q;
+            pos[q] = at;
+        }
+    }
+}
+
+bool route_dispatch_fits(uint32_t experts, uint32_t k, uint32_t tokens) {
+    // route_one_wave keeps no LDS copy of the logits for these sizes
+    return tokens > 0 && experts <= 1024 && k <= (uint32_t)kWave;
+}
+
+hipError_t launch_route_dispatch(Prof *p, hipStream_t s, const float *logits, uint32_t experts,
+                                 uint32_t k, int normalize, uint32_t tokens, uint32_t *ids,
+                                 float *weights, uint32_t *arrive, uint32_t tm, uint32_t *counts,
+                                 uint32_t *offsets, uint32_t *perm, uint32_t *pos, uint32_t *tiles,
+                                 uint32_t *ntiles) {
+    if (!route_dispatch_fits(experts, k, tokens)) return hipErrorInvalidValue;
+    const uint32_t nb = (tokens + kRdWaves - 1) / kRdWaves;
+    return launch_kernel(p, "route_dispatch", route_dispatch_kernel, dim3(nb), dim3(kRdThreads),
+                         (size_t)kRdWaves * experts * sizeof(uint32_t), s, logits, tokens, experts, k,
+                         normalize, ids, weights, arrive, tm, counts, offsets, perm, pos, tiles,
+                         ntiles);
+}
+
 }  // namespace moehip

@@ -72,7 +72,10 @@ moe_status moe_gpu_create(int device, moe_gpu **out) {
         hipStreamCreateWithFlags(&g->side, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreate(&g->ev_begin) != hipSuccess || hipEventCreate(&g->ev_end) != hipSuccess ||
         hipEventCreateWithFlags(&g->ev_fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&g->ev_join, hipEventDisableTiming) != hipSuccess) {
+        hipEventCreateWithFlags(&g->ev_join, hipEventDisableTiming) != hipSuccess ||
+        hipMalloc(reinterpret_cast<void **>(&g->arrive), 256) != hipSuccess ||
+        hipMemset(g->arrive, 0, 256) != hipSuccess) {
+        if (g->arrive) (void)hipFree(g->arrive);
         delete g;
         return MOE_ERR_GPU;
     }
@@ -92,6 +95,7 @@ void moe_gpu_destroy(moe_gpu *g) {
     }
     for (auto e : g->prof.pool) (void)hipEventDestroy(e);
     (void)hipStreamSynchronize(g->side);
+    (void)hipFree(g->arrive);
     (void)hipEventDestroy(g->ev_begin);
     (void)hipEventDestroy(g->ev_end);
     (void)hipEventDestroy(g->ev_fork);

@@ -262,9 +262,14 @@ moe_status run_batched(moe_gpu *g, const moe_block_weights *w, const Dims &d, co
     }
     TRY(launch_seg_rows(p, s, "seg_router", wdesc(w->router), xin, nullptr, nullptr, nullptr, t32, runs,
                         bias, logits));
-    TRY(launch_route(p, s, logits, E, K, w->normalize ? 1 : 0, t32, ids, wts));
-    TRY(launch_dispatch(p, s, ids, t32 * K, E, counts, offsets, perm, pos));
-    TRY(launch_tile_schedule(p, s, offsets, E, seg_tokens(), tiles, ntiles));
+    if (route_dispatch_fits(E, K, t32)) {
+        TRY(launch_route_dispatch(p, s, logits, E, K, w->normalize ? 1 : 0, t32, ids, wts, g->arrive,
+                                  seg_tokens(), counts, offsets, perm, pos, tiles, ntiles));
+    } else {
+        TRY(launch_route(p, s, logits, E, K, w->normalize ? 1 : 0, t32, ids, wts));
+        TRY(launch_dispatch(p, s, ids, t32 * K, E, counts, offsets, perm, pos));
+        TRY(launch_tile_schedule(p, s, offsets, E, seg_tokens(), tiles, ntiles));
+    }
     TRY(launch_seg_gateup(p, s, "seg_gateup", wdesc(w->gate), wdesc(w->up), xin, perm, K, tiles, ntiles,
                           offsets, 0, entries, act));
     TRY(launch_seg_rows(p, s, "seg_down", wdesc(w->down), act, tiles, ntiles, offsets, 0, entries,

@@ -97,6 +97,15 @@ hipError_t launch_route(Prof *p, hipStream_t s, const float *logits, uint32_t ex
 hipError_t launch_dispatch(Prof *p, hipStream_t s, const uint32_t *ids, uint32_t pairs,
                            uint32_t experts, uint32_t *counts, uint32_t *offsets, uint32_t *perm,
                            uint32_t *pos);
+// launch_route, launch_dispatch and launch_tile_schedule (work items of tm
+// pairs) in one launch; `arrive` is a device word that is zero before the
+// launch and is zero again after it.
+bool route_dispatch_fits(uint32_t experts, uint32_t k, uint32_t tokens);
+hipError_t launch_route_dispatch(Prof *p, hipStream_t s, const float *logits, uint32_t experts,
+                                 uint32_t k, int normalize, uint32_t tokens, uint32_t *ids,
+                                 float *weights, uint32_t *arrive, uint32_t tm, uint32_t *counts,
+                                 uint32_t *offsets, uint32_t *perm, uint32_t *pos, uint32_t *tiles,
+                                 uint32_t *ntiles);
 
 // ---- element-wise (k_elem.hip) ----
 hipError_t launch_swiglu(Prof *p, hipStream_t s, const float *a, const float *b, float *y,

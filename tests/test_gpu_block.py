@@ -213,12 +213,35 @@ def test_batched_decode_layouts(gpu, experts, T):
     got = run_block(gpu, bw, x, T, PATH_AUTO, bias=bias)
     prof = gpu.profile_read()
     gpu.profile(False)
-    for k in ("seg_router", "seg_gateup", "seg_down", "seg_shared_gateup", "seg_shared_down"):
+    for k in ("seg_router", "route_dispatch", "seg_gateup", "seg_down", "seg_shared_gateup",
+              "seg_shared_down"):
         assert k in prof and prof[k][0] == 1, k
     check_against_oracle(blk, x, got, bias=bias)
     ref = run_block(gpu, bw, x, T, PATH_GROUPED, bias=bias)
     assert np.array_equal(got[2], ref[2])
     assert rel_max_err(got[0], ref[0]) <= F32_TOL
+
+
+def test_route_dispatch_grids_in_sequence(gpu):
+    """The fused route + dispatch launch counts its finished blocks on a
+    device word that its last block puts back to zero: launches of 1, 18, 2
+    and 1 blocks (T 3, 70, 6, 2) in a row each route and place exactly."""
+    kinds = {"router": DENSE, "experts": (4, 64, BF16), "shared": (8, 32, BF16), "shared_gate": DENSE}
+    blk = HostBlock(256, 24, 4, 128, 64, kinds, seed=91, random_experts=True)
+    bw = blk.upload(gpu)
+    for T in (3, 70, 6, 2):
+        print(f"[case] route_dispatch sequence T={T}", flush=True)
+        x = synth.normal(4700 + T, T * 256).reshape(T, 256)
+        gpu.profile_reset()
+        gpu.profile(True)
+        got = run_block(gpu, bw, x, T, PATH_AUTO)
+        prof = gpu.profile_read()
+        gpu.profile(False)
+        assert "route_dispatch" in prof, T
+        check_against_oracle(blk, x, got, tokens=range(0, T, max(1, T // 12)))
+        ref = run_block(gpu, bw, x, T, PATH_GROUPED)
+        assert np.array_equal(got[2], ref[2])
+        assert rel_max_err(got[0], ref[0]) <= F32_TOL
 
 
 @pytest.mark.parametrize("shared", [0, 2048])
