@@ -364,7 +364,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              f"(see DESIGN.md for how the MoE layer would shard)", file=sys.stderr)
+              f"(the MoE layer would shard by expert, one process per GPU, with an "
+              f"all-reduce of the partial outputs in decode)", file=sys.stderr)
         sys.exit(2)
     steps = max(CHUNK, (args.steps + CHUNK - 1) // CHUNK * CHUNK)
     warm = max(CHUNK, (args.warmup + CHUNK - 1) // CHUNK * CHUNK)
