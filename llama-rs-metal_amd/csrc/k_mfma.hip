@@ -5,7 +5,9 @@
 // (token, k) pairs form one contiguous segment, and each segment runs one GEMM.
 //
 //   to_bf16        x (F32, optionally RMS-normalised) -> bf16 rows (the GEMMs' A)
-//   tile_schedule  segment sizes -> list of (expert, first pair) M-tiles
+//   tile_schedule  segment sizes -> list of (expert, first pair) M-tiles (the
+//                  dispatch kernel writes the same list itself where the
+//                  experts fit its LDS; this kernel serves the other cases)
 //   combine16      out[t] = sum_k w[t, k] * y[pos(t, k)] (+ shared, + residual)
 
 #include "rowdot.hpp"
@@ -178,11 +180,7 @@ hipError_t launch_mfma_experts(Prof *p, hipStream_t s, const WDesc &gate, const 
                                const PackedW &pd, const uint16_t *xb16, uint32_t tokens,
                                const uint32_t *offsets, const uint32_t *perm, uint32_t k,
                                uint32_t *tiles, uint32_t *ntiles, uint16_t *act16, uint16_t *y16) {
-    const uint32_t E = gate.experts;
-    hipError_t e = launch_kernel(p, "tile_schedule", tile_schedule_kernel, dim3(1), dim3(64), 0, s,
-                                 offsets, E, gemm_tile_rows(), tiles, ntiles);
-    if (e != hipSuccess) return e;
-    e = launch_grouped_gemm(p, s, 0, gate, up, pg, pu, xb16, tokens, perm, offsets, tiles, ntiles, k,
+    hipError_t e = launch_grouped_gemm(p, s, 0, gate, up, pg, pu, xb16, tokens, perm, offsets, tiles, ntiles, k,
                             act16);
     if (e != hipSuccess) return e;
     return launch_grouped_gemm(p, s, 1, down, down, pd, pd, act16, (uint64_t)tokens * k, perm, offsets,

@@ -158,6 +158,10 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_place_kernel(
 // expert id; per-wave, per-expert running counts (LDS) carry it across the
 // wave's rounds and a per-expert prefix over the waves across the block.  So
 // perm is ordered by pair index within every expert, as in the two-pass path.
+// With `tiles`, block 0 (which holds every expert's count and offset after
+// its scan) also writes the work list that tile_schedule_kernel would: the
+// (expert, first position) of every run of tm pairs, experts ascending, and
+// their count.
 constexpr int kPlaceThreads = 1024;
 constexpr int kPlaceWaves = kPlaceThreads / 64;
 constexpr int kPlaceRounds = 4;
@@ -166,10 +170,11 @@ constexpr int kHistLoads = 8;  // id loads in flight per thread while histogramm
 
 __global__ __launch_bounds__(kPlaceThreads) void dispatch_kernel(
     const uint32_t *__restrict__ ids, uint32_t pairs, uint32_t E, uint32_t *__restrict__ counts,
-    uint32_t *__restrict__ offsets, uint32_t *__restrict__ perm, uint32_t *__restrict__ pos) {
+    uint32_t *__restrict__ offsets, uint32_t *__restrict__ perm, uint32_t *__restrict__ pos,
+    uint32_t tm, uint32_t *__restrict__ tiles, uint32_t *__restrict__ ntiles) {
     extern __shared__ uint32_t sm[];
     uint32_t *all = sm, *base = sm + E, *cw = sm + 2 * E;  // cw: [kPlaceWaves][E]
-    __shared__ uint32_t wsum[kPlaceWaves];
+    __shared__ uint32_t wsum[kPlaceWaves], tsum[kPlaceWaves];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const uint32_t c0 = blockIdx.x * kPlaceChunk;
     for (uint32_t i = tid; i < (2 + kPlaceWaves) * E; i += kPlaceThreads) sm[i] = 0u;
@@ -219,6 +224,32 @@ __global__ __launch_bounds__(kPlaceThreads) void dispatch_kernel(
         run += c;
     }
     if (blockIdx.x == 0 && tid == 0) offsets[E] = total;
+    if (tiles && blockIdx.x == 0) {  // uniform over the block
+        // block 0 places the first chunk, so base[e] now holds offsets[e]
+        uint32_t tpart = 0;
+        for (uint32_t e = e0; e < e1; e++) tpart += (all[e] + tm - 1) / tm;
+        uint32_t tincl = tpart;
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t v = __shfl_up(tincl, o, 64);
+            if (lane >= o) tincl += v;
+        }
+        if (lane == 63) tsum[wv] = tincl;
+        __syncthreads();
+        uint32_t first = tincl - tpart, ttotal = 0;
+        for (int w = 0; w < kPlaceWaves; w++) {
+            if (w < wv) first += tsum[w];
+            ttotal += tsum[w];
+        }
+        for (uint32_t e = e0; e < e1; e++) {
+            const uint32_t nt = (all[e] + tm - 1) / tm;
+            for (uint32_t i = 0; i < nt; i++) {
+                tiles[2 * (first + i)] = e;
+                tiles[2 * (first + i) + 1] = base[e] + i * tm;
+            }
+            first += nt;
+        }
+        if (tid == 0) *ntiles = ttotal;
+    }
     // ranks inside this chunk: wave wv takes pairs c0 + 64*(kPlaceRounds*wv + r) + lane
     const int bits = 32 - __clz((int)E);  // distinguishes 0..E (E marks an absent pair)
     const uint64_t below = (1ull << lane) - 1ull;
@@ -264,12 +295,16 @@ __global__ __launch_bounds__(kPlaceThreads) void dispatch_kernel(
 
 hipError_t launch_dispatch(Prof *p, hipStream_t s, const uint32_t *ids, uint32_t pairs,
                            uint32_t experts, uint32_t *counts, uint32_t *offsets, uint32_t *perm,
-                           uint32_t *pos) {
+                           uint32_t *pos, uint32_t tm, uint32_t *tiles, uint32_t *ntiles) {
     const size_t lds = (size_t)(2 + kPlaceWaves) * experts * sizeof(uint32_t);
     if (lds <= 48 * 1024) {
         const uint32_t nb = pairs ? (pairs + kPlaceChunk - 1) / kPlaceChunk : 1u;
         return launch_kernel(p, "dispatch", dispatch_kernel, dim3(nb), dim3(kPlaceThreads), lds, s,
-                             ids, pairs, experts, counts, offsets, perm, pos);
+                             ids, pairs, experts, counts, offsets, perm, pos, tm, tiles, ntiles);
+    }
+    if (tiles) {
+        hipError_t e = launch_dispatch(p, s, ids, pairs, experts, counts, offsets, perm, pos);
+        return e != hipSuccess ? e : launch_tile_schedule(p, s, offsets, experts, tm, tiles, ntiles);
     }
     const uint32_t zb = (experts + kDispThreads - 1) / kDispThreads;
     hipError_t e = launch_kernel(p, "dispatch_zero", zero_u32_kernel, dim3(zb), dim3(kDispThreads), 0,

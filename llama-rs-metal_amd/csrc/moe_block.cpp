@@ -267,8 +267,7 @@ moe_status run_batched(moe_gpu *g, const moe_block_weights *w, const Dims &d, co
                                   seg_tokens(), counts, offsets, perm, pos, tiles, ntiles));
     } else {
         TRY(launch_route(p, s, logits, E, K, w->normalize ? 1 : 0, t32, ids, wts));
-        TRY(launch_dispatch(p, s, ids, t32 * K, E, counts, offsets, perm, pos));
-        TRY(launch_tile_schedule(p, s, offsets, E, seg_tokens(), tiles, ntiles));
+        TRY(launch_dispatch(p, s, ids, t32 * K, E, counts, offsets, perm, pos, seg_tokens(), tiles, ntiles));
     }
     TRY(launch_seg_gateup(p, s, "seg_gateup", wdesc(w->gate), wdesc(w->up), xin, perm, K, tiles, ntiles,
                           offsets, 0, entries, act));
@@ -325,7 +324,8 @@ moe_status run_mfma(moe_gpu *g, const moe_block_weights *w, const Dims &d, const
         if (bias) TRY(launch_add(p, s, logits, bias, logits, T * d.E));
         TRY(launch_route(p, s, logits, E, K, w->normalize ? 1 : 0, (uint32_t)T, ids, wts));
     }
-    TRY(launch_dispatch(p, s, ids, (uint32_t)(T * K), E, counts, offsets, perm, pos));
+    TRY(launch_dispatch(p, s, ids, (uint32_t)(T * K), E, counts, offsets, perm, pos,
+                        gemm_tile_rows(), tiles, ntiles));
     // the shared expert needs only the input: side stream, joined before the combine
     const float *so = nullptr, *sgv = nullptr;
     if (w->has_shared) {

@@ -94,9 +94,12 @@ hipError_t launch_gemm_router(Prof *p, hipStream_t s, const WDesc &r, const uint
                               uint32_t tokens, uint32_t ksplit, const float *bias, float *out);
 hipError_t launch_route(Prof *p, hipStream_t s, const float *logits, uint32_t experts, uint32_t k,
                         int normalize, uint32_t tokens, uint32_t *ids, float *weights);
+// With `tiles` it also writes the work list of tm-pair runs that
+// launch_tile_schedule would (in the same launch where the experts fit LDS).
 hipError_t launch_dispatch(Prof *p, hipStream_t s, const uint32_t *ids, uint32_t pairs,
                            uint32_t experts, uint32_t *counts, uint32_t *offsets, uint32_t *perm,
-                           uint32_t *pos);
+                           uint32_t *pos, uint32_t tm = 0, uint32_t *tiles = nullptr,
+                           uint32_t *ntiles = nullptr);
 // launch_route, launch_dispatch and launch_tile_schedule (work items of tm
 // pairs) in one launch; `arrive` is a device word that is zero before the
 // launch and is zero again after it.
@@ -153,6 +156,8 @@ struct PackedW {
 bool pack_layout(const WDesc &w, uint64_t *data_bytes, uint64_t *sb_bytes);
 hipError_t launch_pack_weight(Prof *p, hipStream_t s, const WDesc &w, void *data, void *scales,
                               void *biases);
+// tiles / ntiles: the work list of gemm_tile_rows()-pair M-tiles, written by
+// launch_dispatch (or launch_tile_schedule) over the same offsets.
 hipError_t launch_mfma_experts(Prof *p, hipStream_t s, const WDesc &gate, const WDesc &up,
                                const WDesc &down, const PackedW &pg, const PackedW &pu,
                                const PackedW &pd, const uint16_t *xb16, uint32_t tokens,
