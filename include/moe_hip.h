@@ -97,6 +97,11 @@ uint64_t moe_allocated_bytes(const moe_gpu *gpu);
 /* Human-readable text of the last error on this gpu (the String payload of
  * metal_backend::Error). */
 const char *moe_last_error(const moe_gpu *gpu);
+/* The byte count of Error::Allocation(usize) (crates/metal-backend/src/lib.rs:12-13):
+ * the requested size when the last error on this gpu was MOE_ERR_ALLOCATION
+ * (UINT64_MAX when the element count overflowed, as the reference's
+ * checked_mul failure reports usize::MAX, apple/memory.rs:26), else 0. */
+uint64_t moe_last_error_bytes(const moe_gpu *gpu);
 
 /* ------------------------------------------------------------ memory -- */
 
@@ -250,6 +255,27 @@ typedef struct {
 
 /* Number of 4-byte workspace elements moe_block needs for `tokens`. */
 moe_status moe_block_workspace(const moe_block_weights *w, uint64_t tokens, uint64_t *elems);
+
+/* Where moe_block keeps its routing and dispatch inside the workspace, as
+ * element offsets (no reference counterpart: the reference's scratch slots,
+ * crates/model-runtime/src/workspace.rs:43-50, hold one token's routing and
+ * there is no dispatch).  After a moe_block call over T tokens on a path
+ * that dispatches (every path except the fused single-token decode):
+ *   counts[E], offsets[E+1], perm[T*K], pos[T*K]  u32, as moe_dispatch writes;
+ *   tiles[2*n], ntiles[1]  u32: the work list (expert, first position) of every
+ *   run of `tile_pairs_mfma` (bf16 MFMA path) or `tile_pairs_batched` (batched
+ *   decode) pairs of the non-empty segments, experts ascending, and its
+ *   length n (not written by the VALU grouped path).
+ * logits/ids/weights hold the routing when the io struct gives no outputs. */
+typedef struct {
+    uint64_t logits, ids, weights;
+    uint64_t counts, offsets, perm, pos;
+    uint64_t tiles, ntiles;
+    uint64_t tile_pairs_mfma, tile_pairs_batched;
+    uint64_t total; /* = moe_block_workspace */
+} moe_block_layout;
+moe_status moe_block_workspace_layout(const moe_block_weights *w, uint64_t tokens,
+                                      moe_block_layout *out);
 /* One MoE block over T tokens: out[T, h] from x[T, h] (execute.rs:200-234,
  * token-batched). */
 moe_status moe_block(moe_gpu *gpu, const moe_block_weights *w, moe_buffer x, moe_buffer out,

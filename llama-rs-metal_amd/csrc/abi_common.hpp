@@ -55,6 +55,7 @@ struct moe_gpu {
     bool capturing = false;
     hipEvent_t ev_begin = nullptr, ev_end = nullptr;
     std::string err;
+    uint64_t err_bytes = 0;  // requested bytes of the last allocation error
     std::string name;
     Prof prof;
 };
@@ -67,9 +68,22 @@ struct moe_graph {
 namespace abi {
 
 inline moe_status fail(moe_gpu *g, moe_status st, const std::string &msg) {
-    if (g) g->err = msg;
+    if (g) {
+        g->err = msg;
+        g->err_bytes = 0;
+    }
     return st;
 }
+// Error::Allocation(usize) carries the requested byte count
+// (crates/metal-backend/src/lib.rs:12-13, apple/memory.rs:9-17).
+inline moe_status fail_alloc(moe_gpu *g, uint64_t bytes, const std::string &msg) {
+    fail(g, MOE_ERR_ALLOCATION, msg);
+    if (g) g->err_bytes = bytes;
+    return MOE_ERR_ALLOCATION;
+}
+// n elements of 4 bytes, saturating (the reference's checked_mul(4) failure
+// reports usize::MAX, memory.rs:26)
+inline uint64_t elem_bytes(uint64_t n) { return n > UINT64_MAX / 4 ? UINT64_MAX : n * 4; }
 inline moe_status shape(moe_gpu *g, const std::string &msg) { return fail(g, MOE_ERR_SHAPE, msg); }
 inline moe_status gpu_err(moe_gpu *g, hipError_t e, const char *what) {
     return fail(g, MOE_ERR_GPU, std::string(what) + ": " + hipGetErrorString(e));
@@ -204,10 +218,10 @@ inline moe_status launched(moe_gpu *g, hipError_t e, const char *what) {
 }
 
 inline moe_status alloc_bytes(moe_gpu *g, uint64_t bytes, void **out) {
-    if (bytes == 0 || bytes / 4 > 0xffffffffull * 64) return fail(g, MOE_ERR_ALLOCATION, "allocation size");
+    if (bytes == 0 || bytes / 4 > 0xffffffffull * 64) return fail_alloc(g, bytes, "allocation size");
     void *p = nullptr;
     if (hipMalloc(&p, bytes) != hipSuccess || !p)
-        return fail(g, MOE_ERR_ALLOCATION, "allocation of " + std::to_string(bytes) + " bytes failed");
+        return fail_alloc(g, bytes, "allocation of " + std::to_string(bytes) + " bytes failed");
     g->allocs[reinterpret_cast<uintptr_t>(p)] = Alloc{bytes, true};
     g->live += bytes;
     *out = p;

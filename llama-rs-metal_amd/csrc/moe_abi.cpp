@@ -87,6 +87,7 @@ void moe_gpu_destroy(moe_gpu *g) {
     if (!g) return;
     (void)hipSetDevice(g->device);
     (void)hipStreamSynchronize(g->stream);
+    (void)hipStreamSynchronize(g->side);
     for (auto &a : g->allocs)
         if (a.second.owned) (void)hipFree(reinterpret_cast<void *>(a.first));
     for (auto &q : g->prof.pending) {
@@ -94,7 +95,6 @@ void moe_gpu_destroy(moe_gpu *g) {
         (void)hipEventDestroy(q.b);
     }
     for (auto e : g->prof.pool) (void)hipEventDestroy(e);
-    (void)hipStreamSynchronize(g->side);
     (void)hipFree(g->arrive);
     (void)hipEventDestroy(g->ev_begin);
     (void)hipEventDestroy(g->ev_end);
@@ -115,13 +115,16 @@ uint64_t moe_allocated_bytes(const moe_gpu *g) { return g ? g->live : 0; }
 
 const char *moe_last_error(const moe_gpu *g) { return g ? g->err.c_str() : "no gpu"; }
 
+uint64_t moe_last_error_bytes(const moe_gpu *g) { return g ? g->err_bytes : 0; }
+
 const char *moe_version(void) { return "moe-hip 0.1 (gfx950)"; }
 
 // ================================================================= memory ==
 moe_status moe_zeros(moe_gpu *g, uint64_t n, moe_buffer *out) {
     moe_status st = need_no_batch(g);
     if (st) return st;
-    if (!out || n == 0 || !fits_u32(n)) return fail(g, MOE_ERR_ALLOCATION, "allocation size");
+    if (!out) return shape(g, "null output");
+    if (n == 0 || !fits_u32(n)) return fail_alloc(g, elem_bytes(n), "allocation size");
     void *p = nullptr;
     st = alloc_bytes(g, n * 4, &p);
     if (st) return st;
@@ -134,7 +137,8 @@ moe_status moe_zeros(moe_gpu *g, uint64_t n, moe_buffer *out) {
 moe_status moe_upload(moe_gpu *g, const float *data, uint64_t n, moe_buffer *out) {
     moe_status st = need_no_batch(g);
     if (st) return st;
-    if (!out || !data || n == 0 || !fits_u32(n)) return fail(g, MOE_ERR_ALLOCATION, "allocation size");
+    if (!out || !data) return shape(g, "null pointer");
+    if (n == 0 || !fits_u32(n)) return fail_alloc(g, elem_bytes(n), "allocation size");
     void *p = nullptr;
     st = alloc_bytes(g, n * 4, &p);
     if (st) return st;
@@ -147,7 +151,8 @@ moe_status moe_upload(moe_gpu *g, const float *data, uint64_t n, moe_buffer *out
 moe_status moe_upload_bytes(moe_gpu *g, const void *data, uint64_t bytes, moe_region *out) {
     moe_status st = need_no_batch(g);
     if (st) return st;
-    if (!out || !data || bytes == 0) return fail(g, MOE_ERR_ALLOCATION, "allocation size");
+    if (!out || !data) return shape(g, "null pointer");
+    if (bytes == 0) return fail_alloc(g, 0, "allocation size");
     void *p = nullptr;
     st = alloc_bytes(g, (bytes + 3) & ~3ull, &p);
     if (st) return st;
@@ -193,6 +198,7 @@ moe_status moe_release(moe_gpu *g, const void *base) {
     if (it == g->allocs.end() || !it->second.owned)
         return shape(g, "release of memory this gpu did not allocate");
     (void)hipStreamSynchronize(g->stream);
+    (void)hipStreamSynchronize(g->side);
     hipError_t e = hipFree(const_cast<void *>(base));
     g->live -= it->second.bytes;
     g->allocs.erase(it);

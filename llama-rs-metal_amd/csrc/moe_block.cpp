@@ -135,6 +135,30 @@ WDesc gate_inp_desc(const moe_weight &w) {
         if (e_ != hipSuccess) return gpu_err(g, e_, #expr); \
     } while (0)
 
+// Work forked onto the gpu's side stream (the shared expert) joins the main
+// stream on every exit: at join() on success, else when the guard goes out of
+// scope after a failed launch, so a capture never ends with the side stream
+// still forked and eager work on the side stream is ordered before the main
+// stream's later work.
+struct SideFork {
+    moe_gpu *g;
+    hipStream_t main;
+    bool open = false;
+    hipError_t fork() {
+        hipError_t e = hipEventRecord(g->ev_fork, main);
+        if (e == hipSuccess) e = hipStreamWaitEvent(g->side, g->ev_fork, 0);
+        open = e == hipSuccess;
+        return e;
+    }
+    hipError_t join() {
+        if (!open) return hipSuccess;
+        open = false;
+        hipError_t e = hipEventRecord(g->ev_join, g->side);
+        return e == hipSuccess ? hipStreamWaitEvent(main, g->ev_join, 0) : e;
+    }
+    ~SideFork() { (void)join(); }
+};
+
 // The reference's per-token op sequence (execute.rs:208-233 and encode_dense :251-267).
 moe_status run_ops(moe_gpu *g, const moe_block_weights *w, const Dims &d, const float *xin,
                    const float *xres, float *out, uint64_t T, const moe_block_io *io,
@@ -245,18 +269,17 @@ moe_status run_batched(moe_gpu *g, const moe_block_weights *w, const Dims &d, co
     // the shared expert needs only the input: it runs on the side stream,
     // concurrently with the routed chain, and joins before the combine
     const float *so = nullptr, *sgv = nullptr;
+    SideFork side{g, s};
     if (w->has_shared) {
         float *sh = ws + L.sh_act, *sout = ws + L.sh_out, *sgt = ws + L.sh_gate;
         hipStream_t ss = g->side;
-        TRY(hipEventRecord(g->ev_fork, s));
-        TRY(hipStreamWaitEvent(ss, g->ev_fork, 0));
+        TRY(side.fork());
         TRY(launch_seg_gateup(p, ss, "seg_shared_gateup", wdesc(w->shared_gate), wdesc(w->shared_up), xin,
                               nullptr, 1, nullptr, nullptr, nullptr, t32, runs, sh));
         TRY(launch_seg_rows(p, ss, "seg_shared_down", wdesc(w->shared_down), sh, nullptr, nullptr, nullptr,
                             t32, runs, nullptr, sout));
         TRY(launch_seg_rows(p, ss, "seg_shared_gate", gate_inp_desc(w->shared_gate_inp), xin, nullptr,
                             nullptr, nullptr, t32, runs, nullptr, sgt));
-        TRY(hipEventRecord(g->ev_join, ss));
         so = sout;
         sgv = sgt;
     }
@@ -273,7 +296,7 @@ moe_status run_batched(moe_gpu *g, const moe_block_weights *w, const Dims &d, co
                           offsets, 0, entries, act));
     TRY(launch_seg_rows(p, s, "seg_down", wdesc(w->down), act, tiles, ntiles, offsets, 0, entries,
                         nullptr, yexp));
-    if (w->has_shared) TRY(hipStreamWaitEvent(s, g->ev_join, 0));
+    TRY(side.join());
     TRY(launch_combine(p, s, yexp, pos, wts, K, so, sgv, io->residual ? xres : nullptr, out, t32,
                        (uint32_t)d.h));
     return MOE_OK;
@@ -328,24 +351,23 @@ moe_status run_mfma(moe_gpu *g, const moe_block_weights *w, const Dims &d, const
                         gemm_tile_rows(), tiles, ntiles));
     // the shared expert needs only the input: side stream, joined before the combine
     const float *so = nullptr, *sgv = nullptr;
+    SideFork side{g, s};
     if (w->has_shared) {
         float *sg = ws + L.sh_act, *su = ws + L.sh_up, *sout = ws + L.sh_out, *sgt = ws + L.sh_gate;
         hipStream_t ss = g->side;
-        TRY(hipEventRecord(g->ev_fork, s));
-        TRY(hipStreamWaitEvent(ss, g->ev_fork, 0));
+        TRY(side.fork());
         TRY(launch_gemv(p, ss, wdesc(w->shared_gate), xin, 0, nullptr, 1, sg, (uint32_t)T));
         TRY(launch_gemv(p, ss, wdesc(w->shared_up), xin, 0, nullptr, 1, su, (uint32_t)T));
         TRY(launch_swiglu(p, ss, sg, su, sg, T * d.ffs));
         TRY(launch_gemv(p, ss, wdesc(w->shared_down), sg, 0, nullptr, 1, sout, (uint32_t)T));
         TRY(launch_gemv(p, ss, gate_inp_desc(w->shared_gate_inp), xin, 0, nullptr, 1, sgt, (uint32_t)T));
-        TRY(hipEventRecord(g->ev_join, ss));
         so = sout;
         sgv = sgt;
     }
     TRY(launch_mfma_experts(p, s, wdesc(w->gate), wdesc(w->up), wdesc(w->down), packed(w->gate_packed),
                             packed(w->up_packed), packed(w->down_packed), xb16, (uint32_t)T, offsets, perm,
                             K, tiles, ntiles, act16, y16));
-    if (w->has_shared) TRY(hipStreamWaitEvent(s, g->ev_join, 0));
+    TRY(side.join());
     TRY(launch_combine16(p, s, y16, pos, wts, K, so, sgv, io->residual ? xraw : nullptr, out, (uint32_t)T,
                          (uint32_t)d.h));
     return MOE_OK;
@@ -385,6 +407,17 @@ moe_status moe_block_workspace(const moe_block_weights *w, uint64_t tokens, uint
     const uint64_t h = w->router.dims[0], E = w->router.dims[1], K = w->experts_used;
     const uint64_t ff = w->gate.dims[1], ffs = w->has_shared ? w->shared_gate.dims[1] : 0;
     *elems = ws_layout(tokens, E, K, h, ff, ffs).total;
+    return MOE_OK;
+}
+
+moe_status moe_block_workspace_layout(const moe_block_weights *w, uint64_t tokens,
+                                      moe_block_layout *out) {
+    if (!w || !out || tokens == 0) return MOE_ERR_SHAPE;
+    const uint64_t h = w->router.dims[0], E = w->router.dims[1], K = w->experts_used;
+    const uint64_t ff = w->gate.dims[1], ffs = w->has_shared ? w->shared_gate.dims[1] : 0;
+    const WsLayout L = ws_layout(tokens, E, K, h, ff, ffs);
+    *out = moe_block_layout{L.logits, L.ids,   L.weights, L.counts,         L.offsets,    L.perm,
+                            L.pos,    L.tiles, L.ntiles,  gemm_tile_rows(), seg_tokens(), L.total};
     return MOE_OK;
 }
 

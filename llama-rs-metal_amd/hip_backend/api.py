@@ -44,7 +44,11 @@ class ShapeError(MoeError):
 
 
 class AllocationError(MoeError):
-    pass
+    """Error::Allocation(usize): `bytes` is the requested size."""
+
+    def __init__(self, msg="", bytes=0):
+        super().__init__(msg)
+        self.bytes = bytes
 
 
 _ERRORS = {1: UnavailableError, 2: GpuError, 3: ShapeError, 4: AllocationError}
@@ -98,6 +102,12 @@ class MoeBlockWeightsC(C.Structure):
     ]
 
 
+class MoeBlockLayoutC(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in (
+        "logits", "ids", "weights", "counts", "offsets", "perm", "pos", "tiles", "ntiles",
+        "tile_pairs_mfma", "tile_pairs_batched", "total")]
+
+
 class MoeBlockIOC(C.Structure):
     _fields_ = [
         ("workspace", MoeBufferC),
@@ -122,6 +132,7 @@ SIGNATURES = {
     "moe_gpu_name": (I32, [P, C.c_char_p, C.c_size_t]),
     "moe_allocated_bytes": (U64, [P]),
     "moe_last_error": (C.c_char_p, [P]),
+    "moe_last_error_bytes": (U64, [P]),
     "moe_zeros": (I32, [P, U64, C.POINTER(BUF)]),
     "moe_upload": (I32, [P, P, U64, C.POINTER(BUF)]),
     "moe_upload_bytes": (I32, [P, P, U64, C.POINTER(MoeRegionC)]),
@@ -147,6 +158,7 @@ SIGNATURES = {
     "moe_pack_size": (I32, [C.POINTER(MoeWeightC), C.POINTER(U64), C.POINTER(U64)]),
     "moe_pack_weight": (I32, [P, C.POINTER(MoeWeightC), MoePackedWeightC]),
     "moe_block_workspace": (I32, [C.POINTER(MoeBlockWeightsC), U64, C.POINTER(U64)]),
+    "moe_block_workspace_layout": (I32, [C.POINTER(MoeBlockWeightsC), U64, C.POINTER(MoeBlockLayoutC)]),
     "moe_block": (I32, [P, C.POINTER(MoeBlockWeightsC), BUF, BUF, U64, C.POINTER(MoeBlockIOC)]),
     "moe_profile_enable": (I32, [P, I32]),
     "moe_profile_count": (I32, [P, C.POINTER(U32)]),
@@ -314,10 +326,19 @@ class BlockWeights:
         _check(None, _lib.moe_block_workspace(C.byref(self.c), tokens, C.byref(n)))
         return int(n.value)
 
+    def workspace_layout(self, tokens):
+        """Element offsets of the routing and dispatch inside the workspace
+        (moe_block_workspace_layout) as a dict."""
+        lay = MoeBlockLayoutC()
+        _check(None, _lib.moe_block_workspace_layout(C.byref(self.c), tokens, C.byref(lay)))
+        return {name: int(getattr(lay, name)) for name, _ in MoeBlockLayoutC._fields_}
+
 
 def _check(gpu, status):
     if status != 0:
         msg = _lib.moe_last_error(gpu._h).decode() if gpu is not None else ""
+        if status == 4:
+            raise AllocationError(msg, int(_lib.moe_last_error_bytes(gpu._h)) if gpu is not None else 0)
         raise _ERRORS.get(status, MoeError)(msg)
 
 

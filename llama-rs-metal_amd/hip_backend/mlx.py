@@ -13,7 +13,12 @@ Follows the reference's native MLX reader (crates/model-format/src/mlx/):
   entry overrides the global one (mod.rs:20-27).  Mode must be ``affine``, bits
   2/4/8, and scales and biases must match the packed tensor's leading dims with one
   column per group (mod.rs:51-95);
-- the shared-expert gate ``[1, h]`` is reshaped to ``[h]`` (mod.rs:113-125).
+- the shared-expert gate ``[1, h]`` is reshaped to ``[h]`` (mod.rs:113-125);
+- ``config.json`` (or its ``text_config``) gives the routing semantics as
+  ``mlx/config.rs`` does: ``model_type`` selects the architecture and unknown
+  types are rejected (config.rs:27-44), ``norm_topk_prob`` defaults to true
+  except for Qwen3-Next (config.rs:230-233), ``rms_norm_eps`` to 1e-5
+  (config.rs:93).
 
 Tensors are memory-mapped and uploaded to the GPU as they are: MLX's layout is the
 layout the kernels read, so nothing is repacked.  Only JSON and raw tensor bytes are
@@ -55,6 +60,48 @@ _LAYER = re.compile(r"^model\.layers\.(\d+)\.(.+)$")
 
 def _bad(msg):
     return CheckpointError(msg)
+
+
+def _number(v, key, default=None):
+    """config.rs:7-18: a non-negative integer, the default when absent, at
+    most 1,000,000."""
+    n = v.get(key)
+    if not (isinstance(n, int) and not isinstance(n, bool) and n >= 0):
+        n = default
+    if n is None:
+        raise _bad(f"missing config.{key}")
+    if n > 1_000_000:
+        raise _bad(f"config.{key} exceeds supported limit")
+    return n
+
+
+def _real(v, key, default):
+    """config.rs:19-25: a finite number, the default when absent."""
+    n = v.get(key)
+    n = float(n) if isinstance(n, (int, float)) and not isinstance(n, bool) else float(default)
+    with np.errstate(over="ignore"):
+        n = float(np.float32(n))  # the reference reads the value as f32
+    if not np.isfinite(n):
+        raise _bad(f"nonfinite config.{key}")
+    return n
+
+
+def architecture(root):
+    """config.rs:27-44: the architecture a ``model_type`` selects (the
+    ``text_config`` object, when present, holds the text model's keys)."""
+    text = root.get("text_config", root)
+    kind = root.get("model_type")
+    if not isinstance(kind, str):
+        raise _bad("config.model_type")
+    if kind == "llama":
+        return "llama"
+    if kind in ("qwen3_5", "qwen3_5_text"):
+        return "qwen35moe" if _number(text, "num_experts", 0) > 0 else "qwen35"
+    if kind in ("qwen3_5_moe", "qwen3_5_moe_text"):
+        return "qwen35moe"
+    if kind == "qwen3_next":
+        return "qwen3next"
+    raise CheckpointError(f"MLX model_type {kind}")
 
 
 def _read_json(path):
@@ -208,9 +255,15 @@ class MoeCheckpoint:
         self.directory = directory
         self.config = _read_json(os.path.join(directory, "config.json"))
         text = self.config.get("text_config", self.config)
-        self.experts_used = int(text.get("num_experts_per_tok", 0))  # config.rs:221
-        self.normalize = bool(text.get("norm_topk_prob", False))    # config.rs:230-233
-        self.eps = float(text.get("rms_norm_eps", 1e-6))
+        self.architecture = architecture(self.config)
+        self.experts_used = _number(text, "num_experts_per_tok", 0)  # config.rs:221
+        # config.rs:230-233: Qwen3-Next leaves the top-k weights unnormalised
+        # unless the config asks for it; every other architecture normalises
+        norm = text.get("norm_topk_prob")
+        self.normalize = norm if isinstance(norm, bool) else self.architecture != "qwen3next"
+        self.eps = _real(text, "rms_norm_eps", 1e-5)  # config.rs:93
+        if self.eps <= 0.0:
+            raise _bad("invalid model dimensions or normalization")  # config.rs:94-108
         raw, self.shards = load_raw(directory)
         layers = {}
         for name in raw:

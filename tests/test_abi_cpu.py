@@ -112,3 +112,35 @@ def test_pack_size_is_host_only():
     for c in [w([2048, 768, 128], 4, 64, api.F32), w([2048, 768, 128], 0, 0, 0),
               w([192, 64, 2], 4, 64, api.BF16)]:
         assert lib.moe_pack_size(C.byref(c), C.byref(db), C.byref(sb)) == 3
+
+
+def test_workspace_layout_is_host_only():
+    """moe_block_workspace_layout: the routing and dispatch regions lie inside
+    the workspace, do not overlap, and are large enough for T tokens; the
+    work-list region holds the largest list either tile size can produce."""
+    lib = api.load_library()
+    w = api.MoeBlockWeightsC()
+    w.router.ndims, w.router.dims[0], w.router.dims[1] = 2, 2048, 128
+    w.gate.ndims = 3
+    w.gate.dims[0], w.gate.dims[1], w.gate.dims[2] = 2048, 768, 128
+    w.experts_used = 8
+    T, E, K = 4096, 128, 8
+    lay = api.MoeBlockLayoutC()
+    n = C.c_uint64()
+    assert lib.moe_block_workspace_layout(C.byref(w), T, C.byref(lay)) == 0
+    assert lib.moe_block_workspace(C.byref(w), T, C.byref(n)) == 0
+    assert lay.total == n.value
+    assert lay.tile_pairs_mfma == 128 and lay.tile_pairs_batched == 8
+    worst_tiles = T * K // lay.tile_pairs_batched + E  # one partial run per expert
+    spans = sorted([(lay.logits, T * E), (lay.ids, T * K), (lay.weights, T * K), (lay.counts, E),
+                    (lay.offsets, E + 1), (lay.perm, T * K), (lay.pos, T * K),
+                    (lay.tiles, 2 * worst_tiles), (lay.ntiles, 1)])
+    for (a, na), (b, _) in zip(spans, spans[1:]):
+        assert a + na <= b
+    assert spans[-1][0] + spans[-1][1] <= lay.total
+    assert lib.moe_block_workspace_layout(C.byref(w), 0, C.byref(lay)) == 3
+
+
+def test_error_bytes_without_gpu():
+    lib = api.load_library()
+    assert lib.moe_last_error_bytes(None) == 0

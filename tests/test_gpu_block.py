@@ -22,7 +22,9 @@ F32_TOL = 1e-4
 BF16_TOL = 2e-2  # bf16-MFMA prefill path
 
 
-def run_block(gpu, bw, x, T, path=PATH_AUTO, bias=None, norm_w=None, residual=False):
+def run_block(gpu, bw, x, T, path=PATH_AUTO, bias=None, norm_w=None, residual=False, ws_out=None):
+    """One moe_block call; with `ws_out` (a dict) the workspace's words after
+    the call are stored under "ws" for the in-block dispatch checks."""
     E, K, h = bw.experts, bw.k, bw.hidden
     xb = gpu.upload(x)
     out = gpu.zeros(T * h)
@@ -35,10 +37,52 @@ def run_block(gpu, bw, x, T, path=PATH_AUTO, bias=None, norm_w=None, residual=Fa
                     norm_weight=nb, norm_eps=1e-6, residual=residual, path=path)
     res = (gpu.read(out).reshape(T, h), gpu.read(lo).reshape(T, E),
            gpu.read_u32(io_).reshape(T, K), gpu.read(wo).reshape(T, K))
+    if ws_out is not None:
+        ws_out["ws"] = gpu.read_u32(ws)
     for buf in (xb, out, ws, lo, io_, wo, bb, nb):
         if buf is not None:
             gpu.release(buf)
     return res
+
+
+def tile_schedule(offsets, tm):
+    """(expert, first position) of every run of tm pairs of the non-empty
+    segments, experts ascending (the work list the dispatch writes)."""
+    out = []
+    for e in range(len(offsets) - 1):
+        for q in range(int(offsets[e]), int(offsets[e + 1]), tm):
+            out.append((e, q))
+    return np.array(out, np.uint32).reshape(-1, 2)
+
+
+def check_in_block_dispatch(bw, T, ids, ws, tm=None):
+    """The dispatch moe_block built inside its workspace against the
+    oracle's stable counting sort (orc_dispatch) of the same ids: counts,
+    offsets, perm and pos bit-exact; with `tm`, the work list of tm-pair runs
+    too."""
+    lay = bw.workspace_layout(T)
+    E, K = bw.experts, bw.k
+    counts, offsets, perm, pos = oracle.dispatch(ids, E)
+    got = {n: ws[lay[n]:lay[n] + m] for n, m in (("counts", E), ("offsets", E + 1), ("perm", T * K),
+                                                  ("pos", T * K))}
+    assert np.array_equal(got["counts"], counts)
+    assert np.array_equal(got["offsets"], offsets)
+    assert np.array_equal(got["perm"], perm)
+    assert np.array_equal(got["pos"], pos)
+    if tm is not None:
+        ref = tile_schedule(offsets, tm)
+        n = int(ws[lay["ntiles"]])
+        assert n == len(ref), (n, len(ref))
+        assert np.array_equal(ws[lay["tiles"]:lay["tiles"] + 2 * n].reshape(-1, 2), ref)
+
+
+def check_all_ids(blk, got, normalize=True):
+    """Every token's ids (bit-exact) and weights: the oracle routes the
+    GPU's logits of all T tokens (sampling.metal:1-36)."""
+    _, logits, ids, wts = got
+    ref_ids, ref_w = oracle.route_tokens(logits, blk.K, normalize)
+    assert np.array_equal(ids, ref_ids)
+    np.testing.assert_allclose(wts, ref_w, rtol=2e-6, atol=1e-9)
 
 
 def check_against_oracle(blk, x, got, tokens=None, bias=None, tol=F32_TOL, norm_w=None,
@@ -182,13 +226,20 @@ def c3(gpu):
 
 @pytest.mark.parametrize("T", [1, 8, 32, 64])
 def test_config3_mixed_precision_hot_set(gpu, c3, T):
+    """Config 3 through AUTO (fused decode at 1 token, the batched decode with
+    the fused route + dispatch launch above): every token's ids and output
+    against the oracle, and the dispatch and 8-pair work list built inside
+    the block against orc_dispatch."""
     blk, bw = c3
     print(f"[case] config3 T={T}", flush=True)
     x = synth.normal(2000 + T, T * 2048).reshape(T, 2048)
     bias = hot_bias(T, 512, seed=T)
-    got = run_block(gpu, bw, x, T, PATH_AUTO, bias=bias)
-    sample = range(T) if T <= 8 else range(0, T, T // 8)
-    check_against_oracle(blk, x, got, tokens=sample, bias=bias)
+    wsd = {}
+    got = run_block(gpu, bw, x, T, PATH_AUTO, bias=bias, ws_out=wsd)
+    check_all_ids(blk, got)
+    check_against_oracle(blk, x, got, bias=bias)
+    if T > 1:
+        check_in_block_dispatch(bw, T, got[2], wsd["ws"], tm=bw.workspace_layout(T)["tile_pairs_batched"])
 
 
 @pytest.mark.parametrize("experts", [DENSE, (2, 32, BF16), (2, 128, F32), (4, 32, F16),
@@ -408,19 +459,42 @@ def c4(gpu):
     return blk, blk.upload(gpu)
 
 
-def test_config4_prefill_mfma_zipf(gpu, c4):
+@pytest.mark.parametrize("packed", [False, True])
+def test_config4_prefill_mfma_zipf(gpu, c4, packed):
+    """Config 4 at its real size (4096 tokens, E 128, top 8, ff 768, 4-bit g64
+    bf16, Zipf(1.1) skew) through AUTO (the bf16 MFMA path), over the
+    row-major tensors and over the MFMA tile-order copies the benchmark
+    makes (moe_pack_weight): every token's ids and weights against the
+    oracle's routing of the GPU logits, the dispatch and the 128-pair M-tile
+    list built inside the block against orc_dispatch, outputs of a token
+    sample against the oracle (bf16 tolerance), and the packed run equal to
+    the row-major run bit for bit on every token."""
     blk, bw = c4
     T = 4096
-    print("[case] config4 prefill T=4096 (auto -> bf16 MFMA)", flush=True)
+    if packed:
+        router, gate, up, down = bw.keep[:4]
+        bw = BlockWeights(router, gate, up, down, bw.k, True,
+                          packed=[gpu.pack_weight(w) for w in (gate, up, down)])
+    print(f"[case] config4 prefill T=4096 packed={packed} (auto -> bf16 MFMA)", flush=True)
     x = synth.normal(4000, T * 2048).reshape(T, 2048)
     bias = zipf_bias(T, 128, seed=4)
-    got = run_block(gpu, bw, x, T, PATH_AUTO, bias=bias)
-    sample = list(range(0, T, 256)) + [T - 1]
+    wsd = {}
+    got = run_block(gpu, bw, x, T, PATH_AUTO, bias=bias, ws_out=wsd)
+    check_all_ids(blk, got)
+    check_in_block_dispatch(bw, T, got[2], wsd["ws"], tm=bw.workspace_layout(T)["tile_pairs_mfma"])
+    sample = list(range(0, T, 128)) + [T - 1]
     err = check_against_oracle(blk, x, got, tokens=sample, bias=bias, tol=BF16_TOL,
                                logit_tol=BF16_TOL)
-    print(f"[case] config4 rel err {err:.3e}", flush=True)
+    print(f"[case] config4 packed={packed} rel err {err:.3e}", flush=True)
     counts = np.bincount(got[2].ravel(), minlength=128)
     assert counts.max() > 8 * counts.mean()  # the Zipf skew is realised
+    if packed:
+        ref = run_block(gpu, c4[1], x, T, PATH_AUTO, bias=bias)
+        assert np.array_equal(got[2], ref[2])
+        assert np.array_equal(got[0], ref[0])
+        for pw in bw.packed:
+            for b in pw.buffers:
+                gpu.release(b)
 
 
 @pytest.mark.parametrize("T", [33, 32768])
@@ -561,3 +635,53 @@ def test_mfma_path_8bit_router_norm_residual(gpu, c3):
     got = run_block(gpu, bw, x, T, PATH_MFMA, bias=bias, norm_w=nw, residual=True)
     check_against_oracle(blk, x, got, tokens=range(0, T, 9), bias=bias, tol=BF16_TOL,
                          norm_w=nw, residual=True, logit_tol=BF16_TOL)
+
+
+@pytest.mark.parametrize("E,T,path", [(1024, 1024, PATH_MFMA), (1100, 5, PATH_AUTO), (1100, 40, PATH_GROUPED)])
+def test_dispatch_fallbacks_in_block(gpu, E, T, path):
+    """Expert counts whose dispatch histograms exceed the single-launch
+    dispatch's LDS ((2 + 16) * E words > 48 KiB for E > 682): the MFMA path
+    and the batched decode (which, past 1024 experts, also leaves the fused
+    route + dispatch) take the three-launch dispatch plus the separate
+    work-list kernel; the VALU grouped path the three launches alone.  Ids,
+    dispatch and work list against the oracle, outputs on a token sample."""
+    print(f"[case] dispatch fallback E={E} T={T} path={path}", flush=True)
+    kinds = {"router": DENSE, "experts": (4, 64, BF16), "shared": (4, 64, BF16), "shared_gate": DENSE}
+    blk = HostBlock(256, E, 8, 128, 128, kinds, seed=95, random_experts=True)
+    bw = blk.upload(gpu)
+    x = synth.normal(5300 + T, T * 256).reshape(T, 256)
+    # a hot set of 8 experts for half of the tokens: some segments span several tiles
+    bias = hot_bias(T, E, seed=E + T, frac=0.5, hot=8, boost=6.0)
+    wsd = {}
+    gpu.profile_reset()
+    gpu.profile(True)
+    got = run_block(gpu, bw, x, T, path, bias=bias, ws_out=wsd)
+    prof = gpu.profile_read()
+    gpu.profile(False)
+    assert "dispatch_place" in prof, sorted(prof)
+    lay = bw.workspace_layout(T)
+    tm = {PATH_MFMA: lay["tile_pairs_mfma"], PATH_AUTO: lay["tile_pairs_batched"], PATH_GROUPED: None}[path]
+    if tm is not None:
+        assert "tile_schedule" in prof, sorted(prof)
+    check_all_ids(blk, got)
+    check_in_block_dispatch(bw, T, got[2], wsd["ws"], tm=tm)
+    tol = BF16_TOL if path == PATH_MFMA else F32_TOL
+    check_against_oracle(blk, x, got, tokens=range(0, T, max(1, T // 16)), bias=bias, tol=tol,
+                         logit_tol=tol if path == PATH_MFMA else 1e-5)
+
+
+@pytest.mark.parametrize("T", [300, 2048])
+def test_grouped_and_mfma_dispatch_in_block(gpu, c4, T):
+    """The single-launch dispatch inside the MFMA path and the VALU grouped
+    path (config-4 shapes): dispatch bit-exact against orc_dispatch, the
+    M-tile list against its numpy schedule."""
+    blk, bw = c4
+    x = synth.normal(4700 + T, T * 2048).reshape(T, 2048)
+    bias = zipf_bias(T, 128, seed=6)
+    for path in (PATH_MFMA, PATH_GROUPED):
+        print(f"[case] in-block dispatch T={T} path={path}", flush=True)
+        wsd = {}
+        got = run_block(gpu, bw, x, T, path, bias=bias, ws_out=wsd)
+        check_all_ids(blk, got)
+        tm = bw.workspace_layout(T)["tile_pairs_mfma"] if path == PATH_MFMA else None
+        check_in_block_dispatch(bw, T, got[2], wsd["ws"], tm=tm)

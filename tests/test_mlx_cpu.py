@@ -143,3 +143,64 @@ def test_rejects_truncated_file(tmp_path):
         f.truncate(os.path.getsize(path) - 64)
     with pytest.raises(CheckpointError, match="data offsets"):
         MoeCheckpoint(str(tmp_path))
+
+
+@pytest.mark.parametrize("model_type,arch,normalize", [
+    ("qwen3_next", "qwen3next", False), ("qwen3_5_moe", "qwen35moe", True),
+    ("qwen3_5_moe_text", "qwen35moe", True), ("qwen3_5", "qwen35moe", True)])
+def test_config_defaults_follow_the_reference(tmp_path, model_type, arch, normalize):
+    """Without norm_topk_prob the top-k weights are normalised for every
+    architecture except Qwen3-Next, and rms_norm_eps defaults to 1e-5
+    (crates/model-format/src/mlx/config.rs:93,230-233); "qwen3_5" with
+    num_experts > 0 is the MoE architecture (config.rs:33-39)."""
+    make_checkpoint(str(tmp_path), layers=1, shards=1)
+
+    def strip(c):
+        c["model_type"] = model_type
+        c.pop("norm_topk_prob")
+        c.pop("rms_norm_eps")
+    _config(tmp_path, strip)
+    ck = MoeCheckpoint(str(tmp_path))
+    assert ck.architecture == arch
+    assert ck.normalize is normalize
+    assert ck.eps == pytest.approx(1e-5, rel=1e-7)
+    # an explicit flag wins over the architecture default
+    _config(tmp_path, lambda c: c.update(norm_topk_prob=not normalize))
+    assert MoeCheckpoint(str(tmp_path)).normalize is (not normalize)
+
+
+def test_config_text_config_and_uploaded_block_flag(tmp_path):
+    """A multimodal config keeps the text model's keys in text_config
+    (config.rs:26); the block weights carry the resolved normalize flag."""
+    make_checkpoint(str(tmp_path), layers=1, shards=1)
+
+    def nest(c):
+        text = {k: c.pop(k) for k in ("num_experts", "num_experts_per_tok", "moe_intermediate_size",
+                                      "shared_expert_intermediate_size", "hidden_size",
+                                      "rms_norm_eps", "norm_topk_prob")}
+        text.pop("norm_topk_prob")
+        text["rms_norm_eps"] = 2e-6
+        c["text_config"] = text
+        c["model_type"] = "qwen3_next"
+    _config(tmp_path, nest)
+    ck = MoeCheckpoint(str(tmp_path))
+    assert ck.experts_used == K and ck.normalize is False
+    assert ck.eps == pytest.approx(2e-6, rel=1e-7)
+
+
+@pytest.mark.parametrize("change,match", [
+    (lambda c: c.pop("model_type"), "model_type"),
+    (lambda c: c.update(model_type="mixtral"), "MLX model_type mixtral"),
+    (lambda c: c.update(model_type=7), "model_type"),
+    (lambda c: c.update(rms_norm_eps=0.0), "normalization"),
+    (lambda c: c.update(rms_norm_eps=1e300), "nonfinite"),
+    (lambda c: c.update(num_experts_per_tok=2_000_000), "exceeds supported limit"),
+    (lambda c: c.pop("num_experts_per_tok"), "num_experts_per_tok"),
+])
+def test_config_rejections(tmp_path, change, match):
+    """config.rs:7-44,94-108: model_type is required and must be one the
+    reader knows; eps must be finite and positive; counts are bounded."""
+    make_checkpoint(str(tmp_path), layers=1, shards=1)
+    _config(tmp_path, change)
+    with pytest.raises(CheckpointError, match=match):
+        MoeCheckpoint(str(tmp_path))

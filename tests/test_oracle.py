@@ -124,6 +124,52 @@ def test_matvec_softmax_silu_rmsnorm_closed_forms():
     np.testing.assert_allclose(oracle.rms_norm(x, nw, 1e-5), ref, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("kind", [("dense", F32), ("dense", BF16), (4, 64, BF16), (8, 32, F16),
+                                  (2, 128, F32)])
+@pytest.mark.parametrize("tokens", [1, 3, 17])
+def test_matmul_tokens_vs_independent_float64(kind, tokens):
+    """orc_matmul over several tokens (matrix.rs:63-148: y[t*out + r] =
+    W[r] . x[t*in..]) against a float64 product of the numpy-decoded weight.
+    A wrong token stride (x or y), a transposed weight or a dropped token
+    fails here: every token's row is compared, with distinct inputs."""
+    from helpers import make_tensor
+    inn, out = 256, 24
+    t = make_tensor([inn, out], kind, seed=500 + tokens)
+    x = synth.normal(600 + tokens, tokens * inn).reshape(tokens, inn)
+    if t.bits:
+        wd = _numpy_decode(t).reshape(out, inn)
+    elif t.dtype == F32:
+        wd = t.data.astype(np.float64).reshape(out, inn)
+    else:
+        wd = synth.bf16_bits_to_f32(t.data).astype(np.float64).reshape(out, inn)
+    ref = x.astype(np.float64) @ wd.T
+    got = oracle.matmul(t, x, tokens).reshape(tokens, out)
+    np.testing.assert_allclose(got, ref, rtol=0, atol=2e-5 * np.abs(ref).max())
+    # a shuffled token order is caught (distinct rows)
+    if tokens > 1:
+        assert not np.allclose(got[::-1], ref, rtol=0, atol=2e-5 * np.abs(ref).max())
+
+
+def test_expert_matmul_per_expert_inputs_vs_float64():
+    """orc_expert_matmul: y[k*out + r] = expert ids[k] row r . x (shared input)
+    or . x[k*in..] (per-expert input, the down product), id >= E -> zeros
+    (matrix.rs:149-205, affine.metal:90-91)."""
+    from helpers import make_tensor
+    inn, out, E = 128, 16, 5
+    t = make_tensor([inn, out, E], (4, 32, BF16), seed=77)
+    wd = _numpy_decode(t).reshape(E, out, inn)
+    ids = np.array([3, 0, 7, 3], np.uint32)  # 7 >= E
+    xs = synth.normal(78, 4 * inn).reshape(4, inn)
+    got = oracle.expert_matmul(t, xs, ids, True).reshape(4, out)
+    for k, e in enumerate(ids):
+        ref = wd[e] @ xs[k].astype(np.float64) if e < E else np.zeros(out)
+        np.testing.assert_allclose(got[k], ref, rtol=0, atol=2e-5 * max(1.0, np.abs(ref).max()))
+    got1 = oracle.expert_matmul(t, xs[0], ids, False).reshape(4, out)
+    for k, e in enumerate(ids):
+        ref = wd[e] @ xs[0].astype(np.float64) if e < E else np.zeros(out)
+        np.testing.assert_allclose(got1[k], ref, rtol=0, atol=2e-5 * max(1.0, np.abs(ref).max()))
+
+
 def test_elementwise_closed_forms():
     rng = np.random.default_rng(2)
     a, b = rng.standard_normal(50).astype(np.float32), rng.standard_normal(50).astype(np.float32)
