@@ -281,6 +281,20 @@ moe_status moe_block_workspace_layout(const moe_block_weights *w, uint64_t token
 moe_status moe_block(moe_gpu *gpu, const moe_block_weights *w, moe_buffer x, moe_buffer out,
                      uint64_t tokens, const moe_block_io *io);
 
+/* moe_block without a workspace argument.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * block's scratch is a file-scope device array of MOE_NOALLOC_SCRATCH_BYTES
+ * on every GPU the library runs on, held until the process ends;
+ * io->workspace must be empty, and a shape whose workspace
+ * (moe_block_workspace) exceeds the array fails with MOE_ERR_SHAPE.  The call
+ * allocates nothing.  Every call on one GPU shares that GPU's array: calls on
+ * one moe_gpu are stream ordered, but calls that overlap on one GPU (other
+ * streams, other moe_gpu handles of the same device) race. */
+#define MOE_NOALLOC_SCRATCH_BYTES (64ull << 20)
+moe_status moe_block_noalloc(moe_gpu *gpu, const moe_block_weights *w, moe_buffer x, moe_buffer out,
+                             uint64_t tokens, const moe_block_io *io);
+
 /* ------------------------------------------------------ measurement -- */
 
 /* Per-kernel timing (the analogue of LLAMA_METAL_PROFILE,

@@ -30,6 +30,9 @@ struct Prof {
     std::vector<hipEvent_t> pool;
 };
 void prof_collect(Prof *p, hipStream_t s);
+// Device address of this device's no-allocation scratch array (looked up
+// once per device; the device must be current).
+hipError_t noalloc_scratch_address(int device, void **out);
 
 }  // namespace moehip
 
@@ -49,6 +52,9 @@ struct moe_gpu {
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     // device word of the fused route + dispatch launch: zero between launches
     uint32_t *arrive = nullptr;
+    // this device's copy of the no-allocation scratch array (moe_noalloc.cpp),
+    // null when its address could not be obtained
+    void *scratch = nullptr;
     std::map<uintptr_t, Alloc> allocs;
     uint64_t live = 0;
     bool in_batch = false;
@@ -227,6 +233,12 @@ inline moe_status alloc_bytes(moe_gpu *g, uint64_t bytes, void **out) {
     *out = p;
     return MOE_OK;
 }
+
+// moe_block's checks and dispatch over the paths (moe_block.cpp).  With
+// `scratch`, io->workspace is the library's no-allocation scratch array
+// (moe_noalloc.cpp) rather than a buffer this gpu owns.
+moe_status block_entry(moe_gpu *g, const moe_block_weights *w, moe_buffer x, moe_buffer out,
+                       uint64_t tokens, const moe_block_io *io, bool scratch);
 
 }  // namespace abi
 using namespace abi;

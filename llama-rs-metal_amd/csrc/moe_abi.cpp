@@ -79,6 +79,9 @@ moe_status moe_gpu_create(int device, moe_gpu **out) {
         delete g;
         return MOE_ERR_GPU;
     }
+    // this device's address of the no-allocation scratch (checked; without it
+    // only moe_block_noalloc is unavailable)
+    if (noalloc_scratch_address(device, &g->scratch) != hipSuccess) g->scratch = nullptr;
     *out = g;
     return MOE_OK;
 }

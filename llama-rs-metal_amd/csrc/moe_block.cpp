@@ -423,6 +423,15 @@ moe_status moe_block_workspace_layout(const moe_block_weights *w, uint64_t token
 
 moe_status moe_block(moe_gpu *g, const moe_block_weights *w, moe_buffer x, moe_buffer out,
                      uint64_t tokens, const moe_block_io *io) {
+    return abi::block_entry(g, w, x, out, tokens, io, false);
+}
+
+}  // extern "C"
+
+namespace abi {
+
+moe_status block_entry(moe_gpu *g, const moe_block_weights *w, moe_buffer x, moe_buffer out,
+                       uint64_t tokens, const moe_block_io *io, bool scratch) {
     moe_status st = need_batch(g);
     if (st) return st;
     if (!io) return shape(g, "missing block io");
@@ -432,6 +441,10 @@ moe_status moe_block(moe_gpu *g, const moe_block_weights *w, moe_buffer x, moe_b
     const uint64_t T = tokens;
     if (x.len != T * d.h || out.len != T * d.h) return shape(g, "block input/output length");
     const WsLayout L = ws_layout(T, d.E, d.K, d.h, d.ff, d.ffs);
+    if (scratch && io->workspace.len < L.total)
+        return shape(g, "the block needs " + std::to_string(L.total * 4) +
+                            " bytes of workspace, more than the no-allocation scratch (" +
+                            std::to_string(io->workspace.len * 4) + " bytes)");
     if (io->workspace.len < L.total) return shape(g, "workspace too small");
     if (has(io->logit_bias) && io->logit_bias.len != T * d.E) return shape(g, "logit bias length");
     if (has(io->logits_out) && io->logits_out.len != T * d.E) return shape(g, "logits output length");
@@ -446,7 +459,10 @@ moe_status moe_block(moe_gpu *g, const moe_block_weights *w, moe_buffer x, moe_b
     // ownership
     std::vector<Range> reads{rng(x)};
     std::vector<Range> writes{rng(out), rng(io->workspace)};
-    if ((st = check_own(g, {rng(x), rng(out), rng(io->workspace)}))) return st;
+    if ((st = check_own(g, {rng(x), rng(out)}))) return st;
+    // the no-allocation scratch is the library's own device array, not a
+    // registered allocation
+    if (!scratch && (st = check_own(g, {rng(io->workspace)}))) return st;
     const moe_buffer *opt_in[] = {&io->logit_bias, &io->norm_weight};
     const moe_buffer *opt_out[] = {&io->logits_out, &io->ids_out, &io->weights_out};
     for (auto b : opt_in)
@@ -530,6 +546,10 @@ moe_status moe_block(moe_gpu *g, const moe_block_weights *w, moe_buffer x, moe_b
         return run_batched(g, w, d, xin, xraw, o, T, io, L, ws, logits, ids, wts);
     return run_grouped(g, w, d, xin, xraw, o, T, io, L, ws, logits, ids, wts);
 }
+
+}  // namespace abi
+
+extern "C" {
 
 // ============================================================ profiling ==
 moe_status moe_profile_enable(moe_gpu *g, int enable) {

@@ -160,6 +160,7 @@ SIGNATURES = {
     "moe_block_workspace": (I32, [C.POINTER(MoeBlockWeightsC), U64, C.POINTER(U64)]),
     "moe_block_workspace_layout": (I32, [C.POINTER(MoeBlockWeightsC), U64, C.POINTER(MoeBlockLayoutC)]),
     "moe_block": (I32, [P, C.POINTER(MoeBlockWeightsC), BUF, BUF, U64, C.POINTER(MoeBlockIOC)]),
+    "moe_block_noalloc": (I32, [P, C.POINTER(MoeBlockWeightsC), BUF, BUF, U64, C.POINTER(MoeBlockIOC)]),
     "moe_profile_enable": (I32, [P, I32]),
     "moe_profile_count": (I32, [P, C.POINTER(U32)]),
     "moe_profile_get": (I32, [P, U32, C.c_char_p, C.c_size_t, C.POINTER(U64),
@@ -613,8 +614,24 @@ class Batch:
     def moe_block(self, bw, x, out, tokens, workspace, logit_bias=None, logits_out=None,
                   ids_out=None, weights_out=None, norm_weight=None, norm_eps=1e-6,
                   residual=False, path=PATH_AUTO):
+        io = self._io(workspace, logit_bias, logits_out, ids_out, weights_out, norm_weight, norm_eps,
+                      residual, path)
+        self._ck(_lib.moe_block(self.gpu._h, C.byref(bw.c), x.c, out.c, tokens, C.byref(io)))
+
+    def moe_block_noalloc(self, bw, x, out, tokens, logit_bias=None, logits_out=None, ids_out=None,
+                          weights_out=None, norm_weight=None, norm_eps=1e-6, residual=False,
+                          path=PATH_AUTO):
+        """moe_block with the library's per-GPU scratch array as its workspace
+        (moe_block_noalloc: nothing is allocated)."""
+        io = self._io(None, logit_bias, logits_out, ids_out, weights_out, norm_weight, norm_eps,
+                      residual, path)
+        self._ck(_lib.moe_block_noalloc(self.gpu._h, C.byref(bw.c), x.c, out.c, tokens, C.byref(io)))
+
+    @staticmethod
+    def _io(workspace, logit_bias, logits_out, ids_out, weights_out, norm_weight, norm_eps, residual,
+            path):
         io = MoeBlockIOC()
-        io.workspace = workspace.c
+        io.workspace = _c(workspace)
         io.logit_bias = _c(logit_bias)
         io.logits_out = _c(logits_out)
         io.ids_out = _c(ids_out)
@@ -623,7 +640,7 @@ class Batch:
         io.norm_eps = norm_eps
         io.residual = int(bool(residual))
         io.path = path
-        self._ck(_lib.moe_block(self.gpu._h, C.byref(bw.c), x.c, out.c, tokens, C.byref(io)))
+        return io
 
     def graph(self, graph):
         self._ck(_lib.moe_graph_launch(self.gpu._h, graph.h))
