@@ -8,14 +8,10 @@
 //   GATEUP  act[p, j] = silu(x_t . G_e[j]) * (x_t . U_e[j])   t = perm[p] / K
 //           (activation, crates/metal-backend/src/shaders/elementwise.metal:8-17)
 //   DOWN    y[p, r]   = act_p . D_e[r]   (the combine applies the routing weights)
-//   ROUTER  logits[t, e] = x_t . R_e (+ bias), the router product
-//           (Batch::matmul(router), crates/model-runtime/src/execute.rs:220);
-//           one segment of all tokens, its K split into ksplit ranges whose
-//           F32 partial sums the routing kernel adds in range order
+// (The router product stays F32: k_router.hip.)
 //
 // Work item = kTM pairs of one expert x one N-tile (128 weight rows for
-// grouped_gemm, 64 per wave for affine_gemm) over the full K
-// (ROUTER: over one of its K ranges).
+// grouped_gemm, 64 per wave for affine_gemm) over the full K.
 // Blocks are persistent: the items are split into eight contiguous ranges,
 // one per XCD (workgroup b runs on XCD b % 8), and the blocks of an XCD walk
 // their range together, so the tiles that share an expert's weights and a
@@ -29,8 +25,9 @@
 // reaches LDS by buffer DMA (buffer_load_dwordx4 ... lds), 16-byte chunks
 // XOR-swizzled so the fragment reads are conflict-free.  Two such blocks
 // share a CU; the four waves share one A stage, so per multiply-add half the
-// A bytes of two-wave blocks move into the CU.  grouped_gemm_kernel (ROUTER, dense weights, and tensors whose
-// offsets exceed 32 bits) stages both operands through LDS:
+// A bytes of two-wave blocks move into the CU.  grouped_gemm_kernel (dense
+// weights, and tensors whose offsets exceed 32 bits) stages both operands
+// through LDS:
 //
 // Per 64-wide K step, double-buffered in LDS: the block's threads load the
 // A tile (kTM rows x 128 bytes of bf16, rows gathered through perm for
@@ -77,7 +74,7 @@ constexpr int kAChunks = kTM * kAChunksPerRow / kThreads;  // A chunks one threa
 constexpr int kARowsPerPass = kThreads / kAChunksPerRow;   // A rows one pass covers
 constexpr int kXcds = 8;
 
-enum { GATEUP = 1, DOWN = 2, ROUTER = 3 };
+enum { GATEUP = 1, DOWN = 2 };
 static_assert(kNT % 2 == 0, "gate/up columns pair up inside a wave");
 static_assert(kBVals == 16 || kBVals == 32 || kBVals == 64, "whole words of codes per thread");
 static_assert(kTM * kAChunksPerRow % kThreads == 0, "whole A chunks per thread");
@@ -127,12 +124,8 @@ struct Args {
     const uint32_t *tiles;     // [2*max_tiles] (expert, first position)
     const uint32_t *ntiles;    // number of valid M-tiles (device)
     uint16_t *out;             // GATEUP: act16 [P, ff]; DOWN: y16 [P, h]
-    float *out_f32;            // ROUTER: logits [T, E] (ksplit 1) or partials [ksplit, T, E]
-    const float *bias;         // ROUTER with ksplit 1: optional logit bias [T, E]
     uint32_t k;                // experts per token
     uint32_t n_tiles_n;        // N-tiles per M-tile
-    uint32_t m_total;          // ROUTER: tokens
-    uint32_t ksplit;           // ROUTER: K ranges (nk / ksplit is even)
     PackedW pk, pk2;           // affine GATEUP/DOWN: MFMA tile-order copies of w, w2 (or nulls)
 };
 
@@ -240,8 +233,7 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void grouped_gemm_kernel(Ar
     const uint32_t in = a.w.in, out = a.w.out;
     const uint32_t nk = in / kTK;
     // ---- this block's share of the work items ----
-    const uint32_t n_tiles_m = MODE == ROUTER ? (a.m_total + kTM - 1) / kTM : 0;
-    const uint32_t items = MODE == ROUTER ? n_tiles_m * a.n_tiles_n * a.ksplit : *a.ntiles * a.n_tiles_n;
+    const uint32_t items = *a.ntiles * a.n_tiles_n;
     const uint32_t xcd = blockIdx.x % kXcds, q = blockIdx.x / kXcds, nq = gridDim.x / kXcds;
     const uint32_t per_xcd = (items + kXcds - 1) / kXcds;
     const uint32_t lo = xcd * per_xcd, hi = min(items, lo + per_xcd);
@@ -253,25 +245,9 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void grouped_gemm_kernel(Ar
     const int br = tid / kBPerRow, bq = tid % kBPerRow;
 
     for (uint32_t item = lo + q; item < hi; item += nq) {
-        uint32_t mt, nt, e, m0, seg_end, ks = 0, kbeg = 0, kend = nk;
-        if constexpr (MODE == ROUTER) {
-            // consecutive items: M-tiles sharing one (K range, N-tile) of the router
-            mt = item % n_tiles_m;
-            const uint32_t rest = item / n_tiles_m;
-            nt = rest % a.n_tiles_n;
-            ks = rest / a.n_tiles_n;
-            e = 0;
-            m0 = mt * kTM;
-            seg_end = a.m_total;
-            kbeg = ks * (nk / a.ksplit);
-            kend = kbeg + nk / a.ksplit;
-        } else {
-            mt = item / a.n_tiles_n;
-            nt = item % a.n_tiles_n;
-            e = a.tiles[2 * mt];
-            m0 = a.tiles[2 * mt + 1];
-            seg_end = a.offsets[e + 1];
-        }
+        const uint32_t mt = item / a.n_tiles_n, nt = item % a.n_tiles_n, kbeg = 0, kend = nk;
+        const uint32_t e = a.tiles[2 * mt], m0 = a.tiles[2 * mt + 1];
+        const uint32_t seg_end = a.offsets[e + 1];
         // a wave whose rows all lie past the segment only loads and
         // dequantises (with one or two 64-row wave groups along M the first
         // rows are always live: no branch)
@@ -398,18 +374,6 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void grouped_gemm_kernel(Ar
                             const float g = acc[s][t][r], u = acc[s][t + 1][r];
                             const float act = g * __builtin_amdgcn_rcpf(1.0f + exp_fast(-g)) * u;
                             a.out[(uint64_t)pos * out + j] = (uint16_t)(pack_bf16(act, 0.f) & 0xffffu);
-                        }
-                    }
-                } else if constexpr (MODE == ROUTER) {
-#pragma unroll
-                    for (int t = 0; t < kNT; t++) {
-                        const uint32_t n = nt * kTN + 32 * (kNT * wn + t) + (lane & 31);
-                        if (n >= out) continue;
-                        if (a.ksplit == 1) {
-                            const uint64_t o = (uint64_t)pos * out + n;
-                            a.out_f32[o] = a.bias ? acc[s][t][r] + a.bias[o] : acc[s][t][r];
-                        } else {
-                            a.out_f32[((uint64_t)ks * a.m_total + pos) * out + n] = acc[s][t][r];
                         }
                     }
                 } else {
@@ -761,8 +725,8 @@ struct Launch {
     uint32_t affine_blocks;
     template <int BITS, int T>
     hipError_t operator()() {
-        const char *name = MODE == DOWN ? "gemm_down" : MODE == ROUTER ? "gemm_router" : "gemm_gateup";
-        if constexpr (MODE != ROUTER && BITS != 0) {
+        const char *name = MODE == DOWN ? "gemm_down" : "gemm_gateup";
+        if constexpr (BITS != 0) {
             if (affine)
                 return launch_kernel(p, name, affine_gemm_kernel<MODE, BITS, T>, dim3(affine_blocks),
                                      dim3(kAfThreads), 0, s, a);
@@ -844,34 +808,6 @@ hipError_t launch_grouped_gemm(Prof *p, hipStream_t s, int down, const WDesc &w,
         e = dispatch_kind(w, gemm::Launch<gemm::GATEUP>{p, s, a, blocks, affine, affine_blocks});
     }
     return e;
-}
-
-uint32_t gemm_router_ksplit(const WDesc &r, uint32_t tokens, uint64_t part_floats) {
-    const uint32_t nk = r.in / gemm::kTK;
-    const uint32_t tiles = (tokens + gemm::kTM - 1) / gemm::kTM * ((r.out + gemm::kTN - 1) / gemm::kTN);
-    uint32_t ks = 1;
-    // about two items per block of the persistent grid, each over an even
-    // number of K steps, while the partial sums fit their buffer
-    while (ks < 16 && tiles * ks * 2 < gemm_blocks() && nk % (4 * ks) == 0 &&
-           (uint64_t)(2 * ks) * tokens * r.out <= part_floats)
-        ks *= 2;
-    return ks;
-}
-
-hipError_t launch_gemm_router(Prof *p, hipStream_t s, const WDesc &r, const uint16_t *xb16,
-                              uint32_t tokens, uint32_t ksplit, const float *bias, float *out) {
-    gemm::Args a{};
-    a.w = r;
-    a.w2 = r;
-    a.a_rows = xb16;
-    a.out_f32 = out;
-    a.bias = bias;
-    a.m_total = tokens;
-    a.ksplit = ksplit;
-    a.n_tiles_n = (r.out + gemm::kTN - 1) / gemm::kTN;
-    hipError_t e;
-    if ((e = dispatch_kind(r, SetLds<gemm::ROUTER>{})) != hipSuccess) return e;
-    return dispatch_kind(r, gemm::Launch<gemm::ROUTER>{p, s, a, gemm_blocks(), false, 0});
 }
 
 }  // namespace moehip

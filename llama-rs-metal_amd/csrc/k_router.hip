@@ -1,0 +1,243 @@
+// Router product of the prefill path in F32 on the F32 matrix cores
+// (v_mfma_f32_32x32x2_f32): logits[t, e] = x_t . R_e (+ bias), the reference's
+// Batch::matmul(router) (crates/model-runtime/src/execute.rs:220), which
+// multiplies many tokens in F32 (affine_mm / gemm_simd with float 8x8
+// tiles, crates/metal-backend/src/apple/ops/matrix.rs:77-123).
+//
+// The routing is exact given the logits, so the logits themselves must be F32
+// products: bf16 operands change the selected experts of about 1-2% of the
+// tokens of a 4096-token prefill.  Here both operands stay F32: x as stored
+// (or RMS-normalised, F32), and the router's weights decoded to F32 exactly
+// as Tensor::decode does (w = code * scale + bias, one product and one sum,
+// crates/model-format/src/checkpoint.rs:164-196; F16/BF16 widened exactly).
+// The products are the oracle's; only the summation order differs.
+//
+// Block = kWaves waves; wave w owns the 32x32 tile of 32 tokens x experts
+// e0 + 32w .. +31, over one of `ksplit` K ranges, in iterations of 64 K
+// values.  The block's 32 token rows of an iteration reach LDS through
+// coalesced loads (8 threads per 128-byte row segment), shared by the four
+// waves; each lane loads its own expert row's 32 weight values of the
+// iteration (one 16-byte load at 4 bits).  Lane (i = l % 32, h = l / 32)
+// feeds x[i][32h + s] and R[e][32h + s], s = 0..31, to MFMA s of both lane
+// halves (the same permutation of K on both operands).  x and the weights
+// are loaded two iterations ahead, in a loop without branches; one barrier
+// per iteration.  Token and expert rows past the ends are clamped for the
+// loads and not stored.
+#include <type_traits>
+
+#include "rowdot.hpp"
+
+namespace moehip {
+
+namespace rtr {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWaves = 4;                // expert tiles of 32 per block
+constexpr int kThreads = 64 * kWaves;
+constexpr int kIter = 64;                // K values per iteration (32 per lane half)
+constexpr int kRow = kIter + 4;          // LDS floats per token row (16-byte pad: no bank conflicts)
+constexpr uint32_t kTargetWaves = 2048;  // 2 per SIMD on 256 CUs
+
+// One lane's 32 weight values of one iteration, raw (as loaded).
+template <int BITS, int T>
+struct WRaw {
+    static constexpr int NW = BITS == 0 ? (T == 0 ? 32 : 16) : BITS;
+    uint32_t w[NW];
+    uint32_t s, b;
+};
+
+template <int BITS, int T>
+__device__ __forceinline__ void load_w(const WDesc &r, uint64_t el, WRaw<BITS, T> &o) {
+    // el: the first of the lane's 32 consecutive values (a multiple of 32,
+    // so they share one quantization group)
+    constexpr int NW = WRaw<BITS, T>::NW;
+    const uint8_t *base = reinterpret_cast<const uint8_t *>(r.data);
+    const uint64_t byte = BITS ? el * BITS / 8 : el * (T == 0 ? 4 : 2);
+    if constexpr (NW >= 4) {
+#pragma unroll
+        for (int v = 0; v < NW / 4; v++) {
+            const u32x4 a = reinterpret_cast<const u32x4 *>(base + byte)[v];
+#pragma unroll
+            for (int i = 0; i < 4; i++) o.w[4 * v + i] = a[i];
+        }
+    } else {
+        const u32x2 a = *reinterpret_cast<const u32x2 *>(base + byte);
+        o.w[0] = a[0];
+        o.w[1] = a[1];
+    }
+    if constexpr (BITS != 0) {
+        o.s = load_raw<T>(r.scales, el >> r.gshift);
+        o.b = load_raw<T>(r.biases, el >> r.gshift);
+    }
+}
+
+// Values 16j .. 16j + 15 of the lane's 32 as F32: dense values widened
+// exactly; affine values decoded as code * scale + bias with two roundings
+// (no fused multiply-add), the values Tensor::decode produces.
+template <int BITS, int T>
+__device__ __forceinline__ void decode_w(const WRaw<BITS, T> &o, int j, float *v) {
+    if constexpr (BITS == 0 && T == 0) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) v[i] = __uint_as_float(o.w[16 * j + i]);
+    } else if constexpr (BITS == 0) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            v[2 * i] = raw_to_f32<T>(o.w[8 * j + i] & 0xffffu);
+            v[2 * i + 1] = raw_to_f32<T>(o.w[8 * j + i] >> 16);
+        }
+    } else {
+        float c[16];
+        constexpr int P = 32 / BITS;  // codes per word
+#pragma unroll
+        for (int i = 0; i < 16 / P; i++) unpack_word<BITS>(o.w[(16 / P) * j + i], c + P * i);
+        const float s = raw_to_f32<T>(o.s), b = raw_to_f32<T>(o.b);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+#pragma clang fp contract(off)
+            v[i] = c[i] * s + b;
+        }
+    }
+}
+
+template <int BITS, int T>
+__global__ __launch_bounds__(kThreads) void router_f32_kernel(WDesc r, const float *__restrict__ x,
+                                                              uint32_t tokens, uint32_t ksplit,
+                                                              const float *__restrict__ bias,
+                                                              float *__restrict__ out) {
+    __shared__ __attribute__((aligned(16))) float xs[2][32 * kRow];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const uint32_t i = lane & 31, hf = lane >> 5;
+    const uint32_t h = r.in, E = r.out;
+    const uint32_t t0 = blockIdx.x * 32, e0 = (blockIdx.y * kWaves + wv) * 32;
+    const uint32_t kr = blockIdx.z, klen = h / ksplit, kbeg = kr * klen;
+    const uint32_t iters = klen / kIter;  // even
+    // x staging: thread -> token row tid / 8, 16-byte chunks tid % 8 and
+    // tid % 8 + 8 of the row's 64 values (8 threads read 128 contiguous bytes)
+    const uint32_t srow = tid >> 3, sch = tid & 7;
+    const f32x4 *xg = reinterpret_cast<const f32x4 *>(x + (uint64_t)min(t0 + srow, tokens - 1) * h + kbeg) + sch;
+    // weights: lane (i, hf) holds values 32hf .. 32hf + 31 of the iteration of
+    // expert e0 + i (clamped; rows past E are never stored)
+    const uint64_t wel = (uint64_t)min(e0 + i, E - 1) * h + kbeg + 32 * hf;
+    f32x16 acc = {};
+    f32x4 xr[2][2];  // native vectors: HIP's float4 struct would stay in scratch
+    WRaw<BITS, T> wr[2];
+    auto gload_x = [&](int q, uint32_t it) __attribute__((always_inline)) {
+        xr[q][0] = xg[it * (kIter / 4)];
+        xr[q][1] = xg[it * (kIter / 4) + 8];
+    };
+    auto put_x = [&](int q, int buf) __attribute__((always_inline)) {
+        float *d = &xs[buf][srow * kRow + 4 * sch];
+        *reinterpret_cast<f32x4 *>(d) = xr[q][0];
+        *reinterpret_cast<f32x4 *>(d + 32) = xr[q][1];
+    };
+    // one iteration: MFMA s of half j multiplies x[i][32hf + 16j + s] with
+    // R[e][32hf + 16j + s] (the same permutation of K on both operands)
+    auto compute = [&](int q, int buf) __attribute__((always_inline)) {
+        const float *xrow = &xs[buf][i * kRow + 32 * hf];
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            float wv16[16];
+            decode_w<BITS, T>(wr[q], j, wv16);
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const f32x4 xv = *reinterpret_cast<const f32x4 *>(xrow + 16 * j + 4 * v);
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xv[c], wv16[4 * v + c], acc, 0, 0, 0);
+            }
+        }
+    };
+    // prologue: x of iteration 0 in LDS buffer 0, x of 1 in register stage 1,
+    // weights of 0 and 1 in weight stages 0 and 1
+    gload_x(0, 0);
+    gload_x(1, min(1u, iters - 1));
+    load_w<BITS, T>(r, wel, wr[0]);
+    load_w<BITS, T>(r, wel + (uint64_t)min(1u, iters - 1) * kIter, wr[1]);
+    put_x(0, 0);
+    __syncthreads();
+    // Iteration it (stage Q = it % 2): load x of it + 2 into register stage Q
+    // (its x of `it` went to LDS one iteration earlier); multiply LDS buffer
+    // Q with weight stage Q; load the weights of it + 2 into weight stage Q;
+    // store x of it + 1 (register stage Q ^ 1, loaded one iteration earlier)
+    // into LDS buffer Q ^ 1; one barrier.  Indices past the last iteration
+    // are clamped, so every load is in bounds, and the loop has no branches:
+    // the compiler's in-order wait counts then keep the newest loads in
+    // flight across the store.
+    auto iteration = [&](uint32_t it, auto qc) __attribute__((always_inline)) {
+        constexpr int Q = decltype(qc)::value;
+        gload_x(Q, min(it + 2, iters - 1));
+        __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs
+        compute(Q, Q);
+        load_w<BITS, T>(r, wel + (uint64_t)min(it + 2, iters - 1) * kIter, wr[Q]);
+        put_x(Q ^ 1, Q ^ 1);
+        __syncthreads();
+    };
+    for (uint32_t it = 0; it < iters; it += 2) {
+        iteration(it, std::integral_constant<int, 0>{});
+        iteration(it + 1, std::integral_constant<int, 1>{});
+    }
+    // acc[q] = C[8(q/4) + 4(lane/32) + (q%4)][lane%32]: token row, expert column
+    const uint32_t e = e0 + i;
+    if (e >= E) return;
+#pragma unroll
+    for (int q = 0; q < 16; q++) {
+        const uint32_t t = t0 + 8 * (q >> 2) + 4 * hf + (q & 3);
+        if (t >= tokens) continue;
+        const uint64_t o = (uint64_t)t * E + e;
+        if (ksplit == 1)
+            out[o] = bias ? acc[q] + bias[o] : acc[q];
+        else
+            out[(uint64_t)kr * tokens * E + o] = acc[q];
+    }
+}
+
+struct Launch {
+    Prof *p;
+    hipStream_t s;
+    const WDesc &r;
+    const float *x;
+    uint32_t tokens, ksplit;
+    const float *bias;
+    float *out;
+    template <int BITS, int T>
+    hipError_t operator()() {
+        const dim3 grid((tokens + 31) / 32, (r.out + 32 * kWaves - 1) / (32 * kWaves), ksplit);
+        return launch_kernel(p, "router_f32", router_f32_kernel<BITS, T>, grid, dim3(kThreads), 0, s, r, x,
+                             tokens, ksplit, bias, out);
+    }
+};
+
+}  // namespace rtr
+
+bool router_f32_supported(const WDesc &r, const float *x) {
+    const bool kind = r.bits == 0 ? (r.type == 0 || r.type == 1 || r.type == 30)
+                                  : (r.bits == 2 || r.bits == 4 || r.bits == 8) &&
+                                        (r.type == 0 || r.type == 1 || r.type == 30);
+    // an even number of iterations per K range; 16-byte operand loads (rows
+    // of a multiple of 128 values start 16-byte aligned)
+    return kind && r.in % (2 * rtr::kIter) == 0 && r.experts == 1 &&
+           ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(r.data)) & 15u) == 0;
+}
+
+uint32_t router_f32_ksplit(const WDesc &r, uint32_t tokens, uint64_t part_floats) {
+    const uint64_t waves = (uint64_t)((tokens + 31) / 32) * ((r.out + 31) / 32);
+    uint32_t ks = 1;
+    // K ranges of an even number of iterations, until the grid holds
+    // kTargetWaves waves, while the partial sums fit their buffer
+    while (ks < 16 && waves * ks < rtr::kTargetWaves && r.in % (2 * ks * 2 * rtr::kIter) == 0 &&
+           (uint64_t)(2 * ks) * tokens * r.out <= part_floats)
+        ks *= 2;
+    return ks;
+}
+
+hipError_t launch_router_f32(Prof *p, hipStream_t s, const WDesc &r, const float *x, uint32_t tokens,
+                             uint32_t ksplit, const float *bias, float *out) {
+    if (tokens == 0 || ksplit == 0 || r.in % (ksplit * 2 * rtr::kIter)) return hipErrorInvalidValue;
+    return dispatch_kind(r, rtr::Launch{p, s, r, x, tokens, ksplit, bias, out});
+}
+
+}  // namespace moehip

@@ -329,17 +329,19 @@ moe_status run_mfma(moe_gpu *g, const moe_block_weights *w, const Dims &d, const
     const float *xin = nw ? xn : xraw;  // F32 input of the VALU products
     const WDesc R = wdesc(w->router);
     const float *bias = has(io->logit_bias) ? fp(io->logit_bias) : nullptr;
-    if (gemm_supported(R)) {
+    // the router product stays F32 (the routing is exact given the logits);
+    // only the expert products run in bf16
+    if (router_f32_supported(R, xin)) {
         // partial sums of the K ranges staged in y16, free until the down GEMM
         float *parts = reinterpret_cast<float *>(y16);
         const uint64_t part_floats = (uint64_t)T * K * d.h / 2;
-        const uint32_t ks = gemm_router_ksplit(R, (uint32_t)T, part_floats);
+        const uint32_t ks = router_f32_ksplit(R, (uint32_t)T, part_floats);
         if (ks > 1) {
-            TRY(launch_gemm_router(p, s, R, xb16, (uint32_t)T, ks, nullptr, parts));
+            TRY(launch_router_f32(p, s, R, xin, (uint32_t)T, ks, nullptr, parts));
             TRY(launch_route_sum(p, s, parts, ks, bias, E, K, w->normalize ? 1 : 0, (uint32_t)T,
                                  logits, ids, wts));
         } else {
-            TRY(launch_gemm_router(p, s, R, xb16, (uint32_t)T, 1, bias, logits));
+            TRY(launch_router_f32(p, s, R, xin, (uint32_t)T, 1, bias, logits));
             TRY(launch_route(p, s, logits, E, K, w->normalize ? 1 : 0, (uint32_t)T, ids, wts));
         }
     } else {

@@ -85,13 +85,14 @@ hipError_t launch_hold(hipStream_t s, uint32_t microseconds);
 hipError_t launch_route_sum(Prof *p, hipStream_t s, const float *parts, uint32_t nsplit,
                             const float *bias, uint32_t experts, uint32_t k, int normalize,
                             uint32_t tokens, float *logits, uint32_t *ids, float *weights);
-// Router product on the persistent MFMA GEMM: K split into `ksplit` ranges
-// (gemm_router_ksplit picks it for a partial buffer of `part_floats`); with
-// ksplit 1 `out` receives the logits (+ bias), else the partial sums
-// [ksplit, tokens, E] that launch_route_sum adds.
-uint32_t gemm_router_ksplit(const WDesc &r, uint32_t tokens, uint64_t part_floats);
-hipError_t launch_gemm_router(Prof *p, hipStream_t s, const WDesc &r, const uint16_t *xb16,
-                              uint32_t tokens, uint32_t ksplit, const float *bias, float *out);
+// Router product in F32 on the F32 matrix cores (k_router.hip): K split
+// into `ksplit` ranges (router_f32_ksplit picks it for a partial buffer of
+// `part_floats`); with ksplit 1 `out` receives the logits (+ bias), else the
+// partial sums [ksplit, tokens, E] that launch_route_sum adds.
+bool router_f32_supported(const WDesc &r, const float *x);
+uint32_t router_f32_ksplit(const WDesc &r, uint32_t tokens, uint64_t part_floats);
+hipError_t launch_router_f32(Prof *p, hipStream_t s, const WDesc &r, const float *x, uint32_t tokens,
+                             uint32_t ksplit, const float *bias, float *out);
 hipError_t launch_route(Prof *p, hipStream_t s, const float *logits, uint32_t experts, uint32_t k,
                         int normalize, uint32_t tokens, uint32_t *ids, float *weights);
 // With `tiles` it also writes the work list of tm-pair runs that

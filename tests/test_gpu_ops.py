@@ -222,3 +222,28 @@ def test_elementwise_ops(gpu):
     close(gpu.read(y3), oracle.gate_scalar(a, 0.3), 1e-5)
     close(gpu.read(ym), oracle.mix(xk, wk), 1e-5)
     close(gpu.read(ab), oracle.swiglu(a, bb), 1e-5)
+
+
+def test_allocation_error_carries_bytes(gpu):
+    """Error::Allocation(usize) carries the requested size
+    (crates/metal-backend/src/lib.rs:12-13, apple/memory.rs:9-26): zero-sized
+    and over-limit requests report their byte counts; a later shape error
+    clears it."""
+    from hip_backend import AllocationError, ShapeError
+    with pytest.raises(AllocationError) as e:
+        gpu.zeros(1 << 33)  # more than u32::MAX elements (memory.rs:10)
+    assert e.value.bytes == 4 << 33
+    with pytest.raises(AllocationError) as e:
+        gpu.zeros(0)
+    assert e.value.bytes == 0
+    with pytest.raises(AllocationError) as e:
+        gpu.zeros(1 << 33)
+    b = gpu.zeros(4)
+    with pytest.raises(ShapeError):
+        b.view(2, 8)
+    with pytest.raises(ShapeError):
+        with gpu.batch() as bt:
+            bt.add(b, b.view(0, 2), b)
+    from hip_backend.api import _lib
+    assert _lib.moe_last_error_bytes(gpu._h) == 0
+    gpu.release(b)
