@@ -5,24 +5,31 @@ Workload ("config 2"): Qwen3-Next-shaped MoE layer
 decode at batch 1 -- hidden 2048, 512 experts, top-10 renormalised softmax
 routing, expert ff 512 with SwiGLU, shared expert ff 512 with a sigmoid gate;
 routed and shared expert weights MLX-affine 4-bit g64 with bf16 scales and
-biases, F32 router.  A step is one MoE layer applied to one token.
+biases quantized from seeded N(0, 0.02), F32 router N(0, 0.02), N(0, 1)
+activations.  A step is one MoE layer applied to one token; `value` is the
+steps per second over exactly --steps steps.
 
 Cold-HBM protocol: 8 distinct layers (each with all 512 experts resident,
 ~7.3 GB in total, far beyond the 256 MB Infinity Cache) are rotated step by
-step, every step on a fresh N(0,1) token.  Steps are captured into a HIP graph
-of 64 steps and replayed; the timed region is bracketed by stream
-synchronisation (hipEvents on the library's stream measure it).
+step, every step on a fresh N(0,1) token.  Steps are captured into HIP graphs
+(64 steps, plus one graph of the remainder) and replayed; the timed region is
+bracketed by stream synchronisation (hipEvents on the library's stream).
+Weights are generated on the GPU (hip_backend.probe: the reference fixture
+LCG, Box-Muller, the documented affine quantizer).
 
-Further legs: config 4 prefill (4096 tokens on the bf16 MFMA path; skip with
---no-prefill); config 3, the same layers with 8-bit g64 routers and shared
-experts and hot-set routing, at 1, 8, 32 and 64 concurrent tokens (skip with
---no-batched); config 5, the 48-layer MoE-only stack (RMSNorm, MoE block,
-residual) at the config-2 shapes with 2-bit g32 and 8-bit g128 experts, 256
-decode steps each (skip with --no-stack).
+Further legs: config 4 prefill (4096 tokens on the bf16 MFMA path, eager and
+as a graph replay; skip with --no-prefill); config 3, the same layers with
+8-bit g64 routers and shared experts and hot-set routing, at 1, 8, 32 and 64
+concurrent tokens (--no-batched); config 5, the 48-layer MoE-only stack
+(RMSNorm, MoE block, residual) at the config-2 shapes with 2-bit g32 and 8-bit
+g128 experts, distinct weights per layer, 256 decode steps each (--no-stack).
+The measured peaks (an MFMA-only loop, a streaming HBM read) are reported
+beside the published ones (--no-peaks).
 
 Output: one JSON line (see the driver contract) with the dominant kernel's
 roofline (algorithmic bytes / its hipEvent-measured average duration) and the
-CPU oracle timed on this host's cores.
+CPU oracle timed on this host's cores: single thread and all cores on
+config-2 decode, all cores on a config-4 prefill sample.
 """
 import argparse
 import json
@@ -36,7 +43,7 @@ sys.path.insert(0, PKG)
 
 import numpy as np  # noqa: E402
 
-from hip_backend import BF16, BlockWeights, Gpu, Tensor, synth  # noqa: E402
+from hip_backend import BF16, BlockWeights, Gpu, Tensor, probe, synth  # noqa: E402
 
 METRIC = ("MoE-layer tokens/s + achieved HBM GB/s (decode b=1) and MFMA util (prefill)")
 H, E, K, FF, FFS, BITS, GROUP = 2048, 512, 10, 512, 512, 4, 64
@@ -46,47 +53,60 @@ EXPERT_BYTES_PER_TOKEN = K * 3 * MAT_BYTES + 3 * MAT_BYTES          # 19,464,192
 ROUTER_BYTES = H * E * 4 + H * 4                                    # F32 router + gate row
 GATEUP_BYTES = K * 2 * MAT_BYTES + 2 * MAT_BYTES                    # decode_gateup per launch (routed + shared gate/up)
 HBM_PEAK = 8.0e12
+MFMA_PEAK = 2.5e15   # dense bf16
+F32_MFMA_PEAK = 157.3e12
 CHUNK = 64       # steps per captured graph
 HOLD_US = 40000  # stream hold before a profiled batch (covers its host enqueue)
 LAYERS = 8       # distinct weight sets rotated
+LONG_RUN = 6400  # steps of the steady-state run reported beside `value`
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def make_layer_tensors(seed):
-    """Host tensors of one config-2 layer (router F32 N(0,0.02); shared expert
-    quantised from N(0,0.02); routed experts uniform 4-bit codes with
-    N(0,0.02)-sized group scales -- see hip_backend.synth.random_affine)."""
+def make_layer(gpu, seed):
+    """One config-2 layer on the GPU: F32 router N(0, 0.02); routed and shared
+    experts quantized (4-bit g64 bf16) from N(0, 0.02); F32 shared-expert gate
+    row.  Returns (BlockWeights, [router, gate, up, down, sg, su, sd, gate_row])."""
     s = seed * 100
-    router = Tensor.dense([H, E], synth.normal(s + 1, H * E, 0.0, 0.02))
-    experts = []
-    for i, dims in enumerate(([H, FF, E], [H, FF, E], [FF, H, E])):
-        n = int(np.prod(dims))
-        experts.append(Tensor.affine(dims, *synth.random_affine(s + 2 + i, n, BITS, GROUP, BF16),
-                                     BITS, GROUP, BF16))
-    shared = []
-    for i, dims in enumerate(([H, FFS], [H, FFS], [FFS, H])):
-        n = int(np.prod(dims))
-        shared.append(Tensor.affine(dims, *synth.quantize_affine(
-            synth.normal(s + 5 + i, n, 0.0, 0.02), BITS, GROUP, BF16), BITS, GROUP, BF16))
-    sgate = Tensor.dense([H], synth.normal(s + 8, H, 0.0, 0.02))
-    return router, experts, shared, sgate
+    router = probe.synth_dense_weight(gpu, [H, E], s + 1)
+    experts = [probe.synth_affine_weight(gpu, d, BITS, GROUP, BF16, s + 2 + i)
+               for i, d in enumerate(([H, FF, E], [H, FF, E], [FF, H, E]))]
+    shared = [probe.synth_affine_weight(gpu, d, BITS, GROUP, BF16, s + 5 + i)
+              for i, d in enumerate(([H, FFS], [H, FFS], [FFS, H]))]
+    sgate = gpu.weight_tensor(Tensor.dense([H], synth.normal(s + 8, H, 0.0, 0.02)))
+    bw = BlockWeights(router, experts[0], experts[1], experts[2], K, True, tuple(shared), sgate)
+    return bw, [router, *experts, *shared, sgate]
 
 
-def upload_layer(gpu, tensors):
-    router, experts, shared, sgate = tensors
-    w = [gpu.weight_tensor(t) for t in [router, *experts]]
-    sh = tuple(gpu.weight_tensor(t) for t in shared)
-    return BlockWeights(w[0], w[1], w[2], w[3], K, True, sh, gpu.weight_tensor(sgate))
+def run_graphs(gpu, issue, steps, chunk):
+    """`steps` steps as replays of a captured graph of `chunk` steps plus one
+    graph of the remainder, in one batch; returns the batch's GPU seconds.
+    issue(b, j) issues step j (0 <= j < chunk)."""
+    graphs = []
+    for n in (chunk, steps % chunk):
+        if n == 0 or (n == chunk and steps < chunk):
+            graphs.append(None)
+            continue
+        cap = gpu.capture()
+        with cap as b:
+            for j in range(n):
+                issue(b, j)
+        graphs.append(cap.graph)
+    full, rest = graphs
+    with gpu.batch() as b:
+        for _ in range(steps // chunk):
+            b.graph(full)
+        if rest is not None:
+            b.graph(rest)
+    return b.seconds
 
 
 # ---- config 4: Qwen3-30B-A3B-shaped prefill (bf16 MFMA grouped GEMM) ----
 P_T, P_H, P_E, P_K, P_FF = 4096, 2048, 128, 8, 768
 PREFILL_FLOPS = 2 * P_T * P_K * 3 * P_H * P_FF          # 309,237,645,312 expert FLOPs
 ROUTER_FLOPS = 2 * P_T * P_H * P_E
-MFMA_PEAK = 2.5e15
 
 
 def zipf_bias(tokens, experts, seed, s=1.1):
@@ -96,20 +116,23 @@ def zipf_bias(tokens, experts, seed, s=1.1):
     return np.broadcast_to((-s * np.log(rank)).astype(np.float32), (tokens, experts)).copy()
 
 
-def bench_prefill(gpu, iters=10, packed=True):
-    """Config 4: one MoE layer over 4096 tokens, Zipf(1.1)-skewed routing.
-    With `packed`, the expert weights also get their MFMA tile-order copies
-    (moe_pack_weight, made once before timing), which the MFMA path reads."""
+def prefill_layer(gpu, packed=True):
+    """Config-4 weights on the GPU (4-bit g64 bf16 quantized from N(0, 0.02),
+    router too); with `packed`, also the experts' MFMA tile-order copies
+    (moe_pack_weight), which the MFMA path reads."""
     s = 600 * 100
-    router = Tensor.affine([P_H, P_E], *synth.random_affine(s + 1, P_H * P_E, 4, 64, BF16), 4, 64,
-                           BF16)
-    ex = [Tensor.affine(d, *synth.random_affine(s + 2 + i, int(np.prod(d)), 4, 64, BF16), 4, 64,
-                        BF16)
+    router = probe.synth_affine_weight(gpu, [P_H, P_E], 4, 64, BF16, s + 1)
+    ex = [probe.synth_affine_weight(gpu, d, 4, 64, BF16, s + 2 + i)
           for i, d in enumerate(([P_H, P_FF, P_E], [P_H, P_FF, P_E], [P_FF, P_H, P_E]))]
-    w = [gpu.weight_tensor(t) for t in [router, *ex]]
-    pk = [gpu.pack_weight(t) for t in w[1:]] if packed else None
-    bw = BlockWeights(w[0], w[1], w[2], w[3], P_K, True, packed=pk)
-    x = gpu.upload(synth.normal(6060, P_T * P_H))
+    pk = [gpu.pack_weight(t) for t in ex] if packed else None
+    return BlockWeights(router, ex[0], ex[1], ex[2], P_K, True, packed=pk), [router, *ex]
+
+
+def bench_prefill(gpu, bw, iters=10):
+    """Config 4: one MoE layer over 4096 tokens, Zipf(1.1)-skewed routing,
+    timed eagerly (one moe_block call per layer) and as replays of a captured
+    graph of one layer."""
+    x = probe.synth_normal(gpu, P_T * P_H, 6060)
     out = gpu.zeros(P_T * P_H)
     ws = gpu.zeros(bw.workspace_elems(P_T))
     bias = gpu.upload(zipf_bias(P_T, P_E, 4))
@@ -127,6 +150,15 @@ def bench_prefill(gpu, iters=10, packed=True):
     with gpu.batch() as b:
         for _ in range(iters):
             b.moe_block(bw, x, out, P_T, ws, logit_bias=bias, ids_out=ids)
+    t_eager = b.seconds / iters
+    cap = gpu.capture()
+    with cap as b:
+        b.moe_block(bw, x, out, P_T, ws, logit_bias=bias, ids_out=ids)
+    with gpu.batch() as b:
+        b.graph(cap.graph)
+    with gpu.batch() as b:
+        for _ in range(iters):
+            b.graph(cap.graph)
     t = b.seconds / iters
     counts = np.bincount(gpu.read_u32(ids), minlength=P_E)
     k_us = {k: round(v[1] / v[0] * 1e6, 2) for k, v in prof.items()}
@@ -135,15 +167,19 @@ def bench_prefill(gpu, iters=10, packed=True):
         gpu.release(buf)
     return {
         "workload": "config4: Qwen3-30B-A3B MoE layer prefill, 4096 tokens (h2048 E128 top8 "
-                    "ff768, 4-bit g64 bf16, Zipf(1.1) router skew), path bf16 MFMA",
-        "expert_weights": "MFMA tile-order copies (moe_pack_weight)" if packed else "row-major",
+                    "ff768, 4-bit g64 bf16 quantized from N(0,0.02), Zipf(1.1) router skew), "
+                    "F32 router product, bf16 MFMA expert products",
+        "expert_weights": "MFMA tile-order copies (moe_pack_weight)" if bw.packed else "row-major",
         "tokens_per_s": round(P_T / t, 1),
         "ms_per_layer": round(t * 1e3, 4),
+        "timing": "graph replay of one layer (hipEvents over 10 replays)",
+        "eager_ms_per_layer": round(t_eager * 1e3, 4),
         "expert_flops": PREFILL_FLOPS,
         "achieved_TFLOPs": round(PREFILL_FLOPS / t / 1e12, 2),
         "mfma_frac": round(PREFILL_FLOPS / t / MFMA_PEAK, 4),
         "expert_kernels_TFLOPs": round(PREFILL_FLOPS / expert_s / 1e12, 2) if expert_s else None,
         "expert_kernels_mfma_frac": round(PREFILL_FLOPS / expert_s / MFMA_PEAK, 4) if expert_s else None,
+        "kernels_sum_us": round(sum(k_us.values()), 2),
         "segment_max": int(counts.max()), "segment_min": int(counts.min()),
         "kernels_us": k_us,
     }
@@ -167,14 +203,12 @@ def hot_bias(tokens, seed, frac=0.2, hot=16, boost=8.0):
 
 def c3_layers(gpu, layers):
     """Config-3 layers over the resident config-2 routed experts: 8-bit g64
-    routers and shared experts (quantised from N(0, 0.02)), one per layer."""
+    routers and shared experts quantized from N(0, 0.02), one per layer."""
     out = []
-    for l, bw in enumerate(layers):
+    for l, (bw, _) in enumerate(layers):
         s = 800 * 100 + 10 * l
-        q8 = lambda seed, dims: Tensor.affine(dims, *synth.quantize_affine(
-            synth.normal(seed, int(np.prod(dims)), 0.0, 0.02), 8, GROUP, BF16), 8, GROUP, BF16)
-        router = gpu.weight_tensor(q8(s, [H, E]))
-        shared = tuple(gpu.weight_tensor(q8(s + 1 + i, d))
+        router = probe.synth_affine_weight(gpu, [H, E], 8, GROUP, BF16, s)
+        shared = tuple(probe.synth_affine_weight(gpu, d, 8, GROUP, BF16, s + 1 + i)
                        for i, d in enumerate(([H, FFS], [H, FFS], [FFS, H])))
         sgate = gpu.weight_tensor(Tensor.dense([H], synth.normal(s + 5, H, 0.0, 0.02)))
         _, g, u, d, _, _ = bw.keep
@@ -187,7 +221,7 @@ def bench_batched(gpu, layers, T):
     (fresh N(0,1) tokens and hot-set biases per step) captured into a graph
     and replayed.  Bytes per step: the distinct routed experts the step
     selects (3 matrices each) plus the 8-bit router and shared expert."""
-    xs = gpu.upload(synth.normal(8000 + T, C3_CHUNK * T * H))
+    xs = probe.synth_normal(gpu, C3_CHUNK * T * H, 8000 + T)
     outs = gpu.zeros(C3_CHUNK * T * H)
     bias = gpu.upload(np.concatenate([hot_bias(T, 8100 + 31 * T + j) for j in range(C3_CHUNK)]))
     ids = gpu.zeros(C3_CHUNK * T * K)
@@ -203,16 +237,8 @@ def bench_batched(gpu, layers, T):
     sel = gpu.read_u32(ids).reshape(C3_CHUNK, T * K)
     distinct = [len(np.unique(r)) for r in sel]
     step_bytes = [dn * 3 * MAT_BYTES + 4 * MAT8_BYTES + H * 4 for dn in distinct]
-    cap = gpu.capture()
-    with cap as b:
-        for j in range(C3_CHUNK):
-            issue(b, j)
-    with gpu.batch() as b:
-        b.graph(cap.graph)
-    with gpu.batch() as b:
-        for _ in range(C3_REPS):
-            b.graph(cap.graph)
-    per_step = b.seconds / (C3_REPS * C3_CHUNK)
+    run_graphs(gpu, issue, C3_CHUNK, C3_CHUNK)  # warm
+    per_step = run_graphs(gpu, issue, C3_REPS * C3_CHUNK, C3_CHUNK) / (C3_REPS * C3_CHUNK)
     for buf in (xs, outs, bias, ids, ws):
         gpu.release(buf)
     gbps = np.mean(step_bytes) / per_step / 1e9
@@ -231,28 +257,27 @@ STACK_VARIANTS = {"2bit_g32": (2, 32), "8bit_g128": (8, 128)}
 def bench_stack(gpu, variant):
     """Config 5: 256 decode steps at batch 1, each a fresh N(0,1) hidden state
     through 48 layers of RMSNorm -> MoE block (config-2 shapes) -> residual.
-    The routed and shared expert weights of one seeded random layer are
-    uploaded 48 times (48 distinct HBM copies, all cold for the step); the
-    routers (F32) and norm weights are distinct per layer."""
+    Every layer has its own weights, generated on the GPU: experts and shared
+    expert quantized from N(0, 0.02) at the variant's bits and group (bf16
+    scales and biases), F32 router N(0, 0.02), norm weights 1 + 0.1 N(0, 1)."""
     bits, group = STACK_VARIANTS[variant]
-    s = 700 * 100 + bits
-    ex = [Tensor.affine(d, *synth.random_affine(s + i, int(np.prod(d)), bits, group, BF16), bits, group,
-                        BF16)
-          for i, d in enumerate(([H, FF, E], [H, FF, E], [FF, H, E]))]
-    sh = [Tensor.affine(d, *synth.random_affine(s + 3 + i, int(np.prod(d)), bits, group, BF16), bits,
-                        group, BF16)
-          for i, d in enumerate(([H, FFS], [H, FFS], [FFS, H]))]
-    sgate = Tensor.dense([H], synth.normal(s + 6, H, 0.0, 0.02))
-    layers, norms = [], []
+    s0 = 700 * 100 + bits
+    layers, norms, keep = [], [], []
     for l in range(STACK_LAYERS):
-        router = Tensor.dense([H, E], synth.normal(s + 10 + l, H * E, 0.0, 0.02))
-        w = [gpu.weight_tensor(t) for t in [router, *ex]]
-        layers.append(BlockWeights(w[0], w[1], w[2], w[3], K, True,
-                                   tuple(gpu.weight_tensor(t) for t in sh), gpu.weight_tensor(sgate)))
-        norms.append(gpu.upload((1.0 + 0.1 * synth.normal(s + 100 + l, H)).astype(np.float32)))
+        s = s0 + 1000 * l
+        router = probe.synth_dense_weight(gpu, [H, E], s)
+        ex = [probe.synth_affine_weight(gpu, d, bits, group, BF16, s + 1 + i)
+              for i, d in enumerate(([H, FF, E], [H, FF, E], [FF, H, E]))]
+        sh = [probe.synth_affine_weight(gpu, d, bits, group, BF16, s + 4 + i)
+              for i, d in enumerate(([H, FFS], [H, FFS], [FFS, H]))]
+        sgate = gpu.weight_tensor(Tensor.dense([H], synth.normal(s + 7, H, 0.0, 0.02)))
+        layers.append(BlockWeights(router, ex[0], ex[1], ex[2], K, True, tuple(sh), sgate))
+        keep += [router, *ex, *sh]
+        norms.append(gpu.upload((1.0 + 0.1 * synth.normal(s + 8, H)).astype(np.float32)))
     resident = gpu.allocated_bytes()
-    log(f"[bench] config-5 {variant}: {STACK_LAYERS} layers resident ({resident / 1e9:.1f} GB on the GPU)")
-    xs = gpu.upload(synth.normal(s + 200, STACK_CHUNK * H))
+    log(f"[bench] config-5 {variant}: {STACK_LAYERS} distinct layers resident "
+        f"({resident / 1e9:.1f} GB on the GPU)")
+    xs = probe.synth_normal(gpu, STACK_CHUNK * H, s0 + 200)
     hs = gpu.zeros(STACK_CHUNK * H)
     ws = gpu.zeros(layers[0].workspace_elems(1))
 
@@ -262,20 +287,15 @@ def bench_stack(gpu, variant):
         for l in range(STACK_LAYERS):
             b.moe_block(layers[l], h, h, 1, ws, norm_weight=norms[l], norm_eps=1e-6, residual=True)
 
-    cap = gpu.capture()
-    with cap as b:
-        for j in range(STACK_CHUNK):
-            step(b, j)
-    with gpu.batch() as b:
-        b.graph(cap.graph)
-    with gpu.batch() as b:
-        for _ in range(STACK_STEPS // STACK_CHUNK):
-            b.graph(cap.graph)
-    per_token = b.seconds / STACK_STEPS
+    run_graphs(gpu, step, STACK_CHUNK, STACK_CHUNK)  # warm
+    per_token = run_graphs(gpu, step, STACK_STEPS, STACK_CHUNK) / STACK_STEPS
     mat = lambda i, o: o * i * bits // 8 + 2 * (o * i // group) * 2
-    token_bytes = STACK_LAYERS * ((K + 1) * (2 * mat(H, FF) + mat(FF, H)) + H * E * 4 + H * 4)
-    del layers, norms
     expert_bytes = STACK_LAYERS * (K + 1) * (2 * mat(H, FF) + mat(FF, H))
+    token_bytes = expert_bytes + STACK_LAYERS * (H * E * 4 + H * 4)
+    for w in keep:
+        probe.release(gpu, w)
+    for buf in (*norms, xs, hs, ws):
+        gpu.release(buf)
     return {"variant": variant, "layers": STACK_LAYERS, "steps": STACK_STEPS,
             "expert_bytes_per_token": expert_bytes,
             "us_per_token": round(per_token * 1e6, 2), "tokens_per_s": round(1.0 / per_token, 1),
@@ -283,28 +303,68 @@ def bench_stack(gpu, variant):
             "bytes_per_token": token_bytes,
             "achieved_GBps": round(token_bytes / per_token / 1e9, 1),
             "hbm_frac": round(token_bytes / per_token / HBM_PEAK, 4),
-            "weights": "one seeded random expert set uploaded 48 times; distinct F32 routers and norm weights"}
+            "resident_GB": round(resident / 1e9, 1),
+            "weights": "48 distinct layers generated on the GPU (N(0,0.02) quantized experts and "
+                       "shared experts, F32 routers)"}
 
 
-def cpu_baseline(tensors, budget_s):
-    """The C oracle (single thread) on the same layer, bounded sample."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+# ---- CPU baseline: the C oracle on this host's cores ----
+def host_cores():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))  # the box's CPU share for one GPU is 16
+
+
+def time_oracle(spec, h, tokens_per_call, budget_s, seed0):
     import oracle
-
-    router, experts, shared, sgate = tensors
-    spec = oracle.MoeSpec(router, experts[0], experts[1], experts[2], K, True, tuple(shared), sgate)
-    oracle.build() if not os.path.exists(oracle.LIB_PATH) else None
     n, t0 = 0, time.perf_counter()
     while True:
-        x = synth.normal(900000 + n, H).reshape(1, H)
-        oracle.moe_block(spec, x, 1)
-        n += 1
+        x = synth.normal(seed0 + n, tokens_per_call * h).reshape(tokens_per_call, h)
+        oracle.moe_block(spec, x, tokens_per_call)
+        n += tokens_per_call
         el = time.perf_counter() - t0
-        if el >= budget_s or n >= 10000:
-            break
-    return {"value": n / el, "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"{n} config-2 decode tokens (layer 0 weights, seeds 900000+) through "
-                      f"oracle/moe_oracle.c orc_moe_block, single thread, {el:.1f} s"}
+        if el >= budget_s or n >= 100000:
+            return n, el
+
+
+def cpu_baseline(gpu, layer0, pre, budget_s):
+    """The C oracle (oracle/moe_oracle.c) on host copies of the benchmark's own
+    weights: config-2 decode on one thread and on all cores, and a bounded
+    config-4 prefill sample on all cores (token by token, as the reference's
+    per-token loop runs, crates/model-runtime/src/execute.rs:208)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    if not os.path.exists(oracle.LIB_PATH):
+        oracle.build()
+    bw, ws2 = layer0
+    router, g, u, d, sg, su, sd, sgate = ws2
+    host = [probe.to_host(gpu, w) for w in (router, g, u, d, sg, su, sd)]
+    gate_row = Tensor.dense([H], synth.normal(500 * 100 + 8, H, 0.0, 0.02))
+    spec2 = oracle.MoeSpec(host[0], host[1], host[2], host[3], K, True, tuple(host[4:7]), gate_row)
+    cores = host_cores()
+    oracle.set_threads(1)
+    n1, e1 = time_oracle(spec2, H, 1, budget_s, 900000)
+    oracle.set_threads(cores)
+    nc, ec = time_oracle(spec2, H, 1, budget_s, 910000)
+    res = {"value": round(nc / ec, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
+           "sample": f"{nc} config-2 decode tokens (layer 0 of the benchmark's weights, seeds 910000+) "
+                     f"through oracle/moe_oracle.c orc_moe_block, OpenMP rows over {cores} threads, "
+                     f"{ec:.1f} s",
+           "single_thread": {"value": round(n1 / e1, 3), "unit": "tokens/s", "cores": 1,
+                             "sample": f"{n1} config-2 decode tokens, one thread, {e1:.1f} s"}}
+    if pre is not None:
+        pbw, pws = pre
+        ph = [probe.to_host(gpu, w) for w in pws]
+        spec4 = oracle.MoeSpec(ph[0], ph[1], ph[2], ph[3], P_K, True)
+        np_, ep = time_oracle(spec4, P_H, 1, budget_s, 920000)
+        res["prefill"] = {"value": round(np_ / ep, 3), "unit": "tokens/s", "cores": cores,
+                          "sample": f"{np_} config-4 tokens (the benchmark's prefill weights, "
+                                    f"token by token) on {cores} threads, {ep:.1f} s"}
+    oracle.set_threads(cores)
+    res["host_cpus"] = os.cpu_count()
+    return res
 
 
 COPY_BYTES = 256 << 20  # calibration copy: reads and writes 256 MiB
@@ -318,17 +378,21 @@ def traffic_probe(gpu, which):
     src = gpu.zeros(COPY_BYTES // 4)
     dst = gpu.zeros(COPY_BYTES // 4)
     if which == "decode":
-        layers = [upload_layer(gpu, make_layer_tensors(500 + l)) for l in range(LAYERS)]
-        xs = gpu.upload(synth.normal(4242, CHUNK * H))
+        layers = [make_layer(gpu, 500 + l)[0] for l in range(LAYERS)]
+        xs = probe.synth_normal(gpu, CHUNK * H, 4242)
         outs = gpu.zeros(CHUNK * H)
         ws = gpu.zeros(layers[0].workspace_elems(1))
         with gpu.batch() as b:
             for j in range(CHUNK):
                 b.moe_block(layers[j % LAYERS], xs.view(j * H, H), outs.view(j * H, H), 1, ws)
         log(f"[probe] {CHUNK} eager config-2 decode steps done")
-    else:
-        bench_prefill(gpu, iters=1)
+    elif which == "prefill":
+        bench_prefill(gpu, prefill_layer(gpu)[0], iters=1)
         log("[probe] config-4 prefill done")
+    else:  # the peak probes, short (MFMA counters calibrate against them)
+        log(f"[probe] bf16 MFMA {probe.mfma_peak('bf16', iters=2000, reps=1):.1f} TFLOP/s, "
+            f"F32 MFMA {probe.mfma_peak('f32', iters=200, reps=1):.1f} TFLOP/s, "
+            f"read {probe.hbm_read(1 << 30, reps=1):.1f} GB/s")
     with gpu.batch() as b:
         for _ in range(4):
             b.copy(src, dst)
@@ -349,48 +413,58 @@ def committed_traffic(kernel_prefix):
     return None
 
 
+def peaks():
+    """This GPU's measured rates beside the published MI355X peaks."""
+    return {"hbm_read_GBps": round(probe.hbm_read(4 << 30, reps=5), 1),
+            "mfma_bf16_TFLOPs": round(probe.mfma_peak("bf16"), 1),
+            "mfma_f32_TFLOPs": round(probe.mfma_peak("f32"), 1),
+            "published": {"hbm_GBps": HBM_PEAK / 1e9, "mfma_bf16_TFLOPs": MFMA_PEAK / 1e12,
+                          "mfma_f32_TFLOPs": F32_MFMA_PEAK / 1e12},
+            "method": "hip_backend.probe: a streaming 16-byte-load read of 4 GiB, and MFMA-only loops "
+                      "(4 independent 32x32 accumulators per wave, 8 four-wave blocks per CU); best of "
+                      "5 / 3 timed launches"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=12800)
     ap.add_argument("--warmup", type=int, default=640)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-stack", action="store_true")
     ap.add_argument("--no-batched", action="store_true")
-    ap.add_argument("--traffic-probe", choices=["decode", "prefill"], default=None,
-                    help="short eager workload for rocprofv3 --pmc runs (no timing output)")
+    ap.add_argument("--no-peaks", action="store_true")
+    ap.add_argument("--traffic-probe", choices=["decode", "prefill", "peaks"], default=None,
+                    help="short workload for rocprofv3 --pmc runs (no timing output)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               f"(the MoE layer would shard by expert, one process per GPU, with an "
               f"all-reduce of the partial outputs in decode)", file=sys.stderr)
         sys.exit(2)
-    steps = max(CHUNK, (args.steps + CHUNK - 1) // CHUNK * CHUNK)
-    warm = max(CHUNK, (args.warmup + CHUNK - 1) // CHUNK * CHUNK)
+    if args.steps < 1 or args.warmup < 0:
+        print("bench.py: --steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+        sys.exit(2)
+    steps, warm = args.steps, args.warmup
 
     gpu = Gpu(0)
     if args.traffic_probe:
         traffic_probe(gpu, args.traffic_probe)
         gpu.close()
         return
-    log(f"[bench] device {gpu.name}; building {LAYERS} config-2 layers")
-    layers, host0 = [], None
+    log(f"[bench] device {gpu.name}; generating {LAYERS} config-2 layers on the GPU")
+    layers = []
     for l in range(LAYERS):
-        t = make_layer_tensors(500 + l)
-        layers.append(upload_layer(gpu, t))
-        if l == 0:
-            host0 = t
+        layers.append(make_layer(gpu, 500 + l))
         log(f"[bench] layer {l} resident ({gpu.allocated_bytes() / 1e9:.2f} GB)")
-    xs = gpu.upload(synth.normal(4242, CHUNK * H))
+    xs = probe.synth_normal(gpu, CHUNK * H, 4242)
     outs = gpu.zeros(CHUNK * H)
-    ws = gpu.zeros(layers[0].workspace_elems(1))
+    ws = gpu.zeros(layers[0][0].workspace_elems(1))
 
     def issue(b, j):
-        x = xs.view(j * H, H)
-        o = outs.view(j * H, H)
-        b.moe_block(layers[j % LAYERS], x, o, 1, ws)
+        b.moe_block(layers[j % LAYERS][0], xs.view(j * H, H), outs.view(j * H, H), 1, ws)
 
     # per-kernel durations: hipEvents around each launch on the library's
     # stream, with the stream held until all CHUNK steps are enqueued so that
@@ -416,24 +490,16 @@ def main():
             issue(b, j)
     eager_s = b.seconds / CHUNK
 
-    cap = gpu.capture()
-    with cap as b:
-        for j in range(CHUNK):
-            issue(b, j)
-    graph = cap.graph
-    with gpu.batch() as b:
-        for _ in range(warm // CHUNK):
-            b.graph(graph)
+    if warm:
+        run_graphs(gpu, issue, warm, CHUNK)
     log(f"[bench] warmup {warm} steps done")
     t0 = time.perf_counter()
-    with gpu.batch() as b:
-        for _ in range(steps // CHUNK):
-            b.graph(graph)
+    gpu_s = run_graphs(gpu, issue, steps, CHUNK)
     wall = time.perf_counter() - t0
-    gpu_s = b.seconds
-    log(f"[bench] timed {steps} steps: {gpu_s * 1e3:.2f} ms (events), {wall * 1e3:.2f} ms (wall)")
+    log(f"[bench] timed {steps} steps: {gpu_s * 1e3:.3f} ms (events), {wall * 1e3:.3f} ms (wall)")
     elapsed = max(gpu_s, 1e-12)
     per_step = elapsed / steps
+    long_s = run_graphs(gpu, issue, LONG_RUN, CHUNK) / LONG_RUN
 
     dom = "decode_gateup"
     dom_s = kernels.get(dom)
@@ -462,7 +528,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic",
+        "data": "synthetic (seeded N(0,0.02) weights quantized to 4-bit g64 on the GPU, N(0,1) tokens)",
         "config": {"workload": "config2: Qwen3-Next MoE layer decode b=1 (h2048 E512 top10 "
                                "ff512 + shared ff512, 4-bit g64 bf16, F32 router)",
                    "layers_rotated": LAYERS, "graph_steps": CHUNK, "path": "fused decode"},
@@ -470,16 +536,20 @@ def main():
                       "all_bytes_per_token": EXPERT_BYTES_PER_TOKEN + ROUTER_BYTES,
                       "achieved_GBps": round(layer_gbps, 1),
                       "frac": round(layer_gbps * 1e9 / HBM_PEAK, 4)},
+        "long_run": {"steps": LONG_RUN, "ms_per_step": round(long_s * 1e3, 6),
+                     "tokens_per_s": round(1.0 / long_s, 1)},
         "eager_ms_per_step": round(eager_s * 1e3, 6),
         "kernels_us": {k: round(v * 1e6, 3) for k, v in kernels.items()},
         "roofline": roof,
         "cpu_baseline": None,
     }
+    pre = None
     if not args.no_prefill:
-        log("[bench] config-4 prefill (bf16 MFMA)")
-        result["prefill"] = bench_prefill(gpu)
-        log(f"[bench] prefill: {result['prefill']['ms_per_layer']} ms/layer, "
-            f"{result['prefill']['achieved_TFLOPs']} TFLOP/s")
+        log("[bench] config-4 prefill (F32 router, bf16 MFMA experts)")
+        pre = prefill_layer(gpu)
+        result["prefill"] = bench_prefill(gpu, pre[0])
+        log(f"[bench] prefill: {result['prefill']['ms_per_layer']} ms/layer (graph), "
+            f"{result['prefill']['eager_ms_per_layer']} ms eager, {result['prefill']['achieved_TFLOPs']} TFLOP/s")
     if not args.no_batched:
         c3 = c3_layers(gpu, layers)
         result["batched"] = []
@@ -489,17 +559,25 @@ def main():
                 f"{r['achieved_GBps']} GB/s over {r['distinct_experts_per_step']} experts")
             result["batched"].append(r)
         del c3
+    if not args.no_peaks:
+        result["peaks"] = peaks()
+        log(f"[bench] peaks: {result['peaks']}")
+        if "prefill" in result:
+            p = result["prefill"]
+            p["mfma_frac_of_measured_peak"] = round(p["achieved_TFLOPs"] / result["peaks"]["mfma_bf16_TFLOPs"], 4)
+    if not args.no_cpu:
+        log("[bench] timing the CPU oracle")
+        result["cpu_baseline"] = cpu_baseline(gpu, layers[0], pre, args.cpu_seconds)
     if not args.no_stack:
+        for bw, ws_ in layers[1:]:
+            for w in ws_[:7]:
+                probe.release(gpu, w)  # room for the stack
         result["stack"] = []
         for v in STACK_VARIANTS:
             r = bench_stack(gpu, v)
             log(f"[bench] config-5 {v}: {r['us_per_token']} us/token over {STACK_LAYERS} layers, "
                 f"{r['achieved_GBps']} GB/s")
             result["stack"].append(r)
-    if not args.no_cpu:
-        log("[bench] timing the CPU oracle")
-        result["cpu_baseline"] = cpu_baseline(host0, args.cpu_seconds)
-        result["cpu_baseline"]["host_cpus"] = os.cpu_count()
     print(json.dumps(result), flush=True)
     gpu.close()
 

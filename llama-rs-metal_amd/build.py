@@ -2,7 +2,8 @@
 
 Every translation unit under csrc/ is compiled in parallel into _build/ and
 linked into llama-rs-metal_amd/libmoe_hip.so (in-tree, so it travels with the
-repository snapshot to the GPU box).  Always rebuilds.
+repository snapshot to the GPU box); probe/ (the benchmark's measurement
+and synthetic-weight helpers) becomes libmoe_probe.so.  Always rebuilds.
 """
 import concurrent.futures as cf
 import glob
@@ -15,6 +16,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmoe_hip.so")
+PROBE = os.path.join(HERE, "probe")
+PROBE_LIB = os.path.join(HERE, "libmoe_probe.so")
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 FLAGS = [
@@ -41,23 +44,31 @@ def _compile(src):
     return obj, msgs
 
 
+def _link(objs, lib):
+    tmp = lib + ".tmp"
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
+    os.replace(tmp, lib)
+
+
 def build(verbose=False):
+    """Compiles csrc/ into libmoe_hip.so and probe/ (bench.py's measurement
+    and synthetic-weight helpers, not the MoE ABI) into libmoe_probe.so."""
     os.makedirs(BUILD, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.cpp")))
-    jobs = min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
+    probe_srcs = sorted(glob.glob(os.path.join(PROBE, "*.hip")))
+    jobs = min(len(srcs) + len(probe_srcs), max(1, min(8, os.cpu_count() or 1)))
     with cf.ThreadPoolExecutor(jobs) as ex:
-        results = list(ex.map(_compile, srcs))
+        results = list(ex.map(_compile, srcs + probe_srcs))
     if verbose:
         for obj, msgs in results:
             if msgs.strip():
                 print(msgs)
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp,
-           *[o for o, _ in results]]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
-    os.replace(tmp, LIB)
+    objs = [o for o, _ in results]
+    _link(objs[:len(srcs)], LIB)
+    _link(objs[len(srcs):], PROBE_LIB)
     return LIB
 
 

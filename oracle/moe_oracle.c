@@ -11,8 +11,16 @@
 #include "moe_oracle.h"
 
 #include <math.h>
+#include <omp.h>
 #include <stdlib.h>
 #include <string.h>
+
+/* Loops over at least this many elements run on the OpenMP threads (the
+ * all-core CPU baseline); smaller ones stay on one thread. */
+#define ORC_PAR_MIN 65536
+
+void orc_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
+int orc_threads(void) { return omp_get_max_threads(); }
 
 /* ---------------------------------------------------------------- dtypes -- */
 
@@ -125,13 +133,17 @@ int orc_weight_decode_rows(const orc_weight *w, uint64_t row0, uint64_t nrows, f
     uint64_t n = elements(w);
     if ((row0 + nrows) * in > n) return -1;
     uint64_t i0 = row0 * in, i1 = (row0 + nrows) * in;
+    /* elements are independent: threads split the range (same values as one
+     * thread) */
     if (w->bits == 0) {
+#pragma omp parallel for schedule(static) if (i1 - i0 >= ORC_PAR_MIN)
         for (uint64_t i = i0; i < i1; i++) out[i - i0] = scalar_at(w->data, i, w->dtype);
         return 0;
     }
     const uint32_t *words = (const uint32_t *)w->data;
     uint32_t per_word = 32 / w->bits;
     uint32_t mask = (1u << w->bits) - 1;
+#pragma omp parallel for schedule(static) if (i1 - i0 >= ORC_PAR_MIN)
     for (uint64_t i = i0; i < i1; i++) {
         uint32_t value = words[i / per_word];
         uint32_t code = (value >> ((uint32_t)(i % per_word) * w->bits)) & mask;
@@ -145,8 +157,11 @@ int orc_weight_decode_rows(const orc_weight *w, uint64_t row0, uint64_t nrows, f
 /* ----------------------------------------------------------- tensor-core -- */
 
 /* tensor_core::matvec (crates/tensor-core/src/lib.rs:80-85): rows of `in`
- * elements, each a sequential f32 sum of products. */
+ * elements, each a sequential f32 sum of products.  Rows are independent:
+ * threads split them, and every row's sum keeps its sequential order, so the
+ * result is the single-thread result bit for bit. */
 void orc_matvec(const float *w, const float *x, uint64_t rows, uint64_t in, float *y) {
+#pragma omp parallel for schedule(static) if (rows * in >= ORC_PAR_MIN)
     for (uint64_t r = 0; r < rows; r++) {
         const float *row = w + r * in;
         float s = 0.0f;

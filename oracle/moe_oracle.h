@@ -58,6 +58,11 @@ typedef struct {
     uint64_t dims[3];
 } orc_weight;
 
+/* Threads of the parallel loops (decode, matvec): 1 gives the scalar
+ * single-thread baseline; results do not depend on it. */
+void orc_set_threads(int n);
+int orc_threads(void);
+
 float orc_f16_to_f32(uint16_t h);
 float orc_bf16_to_f32(uint16_t h);
 uint16_t orc_f32_to_bf16(float f);

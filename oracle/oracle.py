@@ -105,6 +105,8 @@ def _declare(L):
         "orc_normal": (None, [U64, U64, F32, F32, P]),
         "orc_quantize_affine": (I32, [P, U64, U32, U32, U32, P, P, P]),
         "orc_affine_pattern": (I32, [U64, U32, U32, U32, P, P, P]),
+        "orc_set_threads": (None, [I32]),
+        "orc_threads": (I32, []),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -390,3 +392,12 @@ def affine_pattern(n, bits, group, scale_type):
     if rc:
         raise ValueError("pattern")
     return packed, scales, biases
+
+
+def set_threads(n):
+    """Threads of the oracle's parallel loops (1: the scalar baseline)."""
+    lib().orc_set_threads(int(n))
+
+
+def threads():
+    return int(lib().orc_threads())

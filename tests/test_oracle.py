@@ -373,3 +373,21 @@ def test_moe_stack_residual():
     xn = np.stack([oracle.rms_norm(r, nw, 1e-6) for r in x])
     out, *_ = oracle.moe_block(blk.spec(), xn, 4)
     np.testing.assert_allclose(h, x + out, rtol=1e-6, atol=1e-6)
+
+
+def test_threads_do_not_change_results():
+    """The oracle's row-parallel loops (the all-core CPU baseline) give the
+    single-thread results bit for bit: every row keeps its sequential sum."""
+    kinds = {"router": DENSE, "experts": (4, 64, BF16), "shared": (8, 64, BF16), "shared_gate": DENSE}
+    blk = HostBlock(512, 64, 4, 512, 256, kinds, seed=33)
+    x = synth.normal(34, 3 * 512).reshape(3, 512)
+    n = oracle.threads()
+    try:
+        oracle.set_threads(1)
+        one = oracle.moe_block(blk.spec(), x, 3)
+        oracle.set_threads(max(4, n))
+        many = oracle.moe_block(blk.spec(), x, 3)
+    finally:
+        oracle.set_threads(n)
+    for a, b in zip(one, many):
+        assert np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32))
