@@ -128,61 +128,90 @@ def prefill_layer(gpu, packed=True):
     return BlockWeights(router, ex[0], ex[1], ex[2], P_K, True, packed=pk), [router, *ex]
 
 
-def bench_prefill(gpu, bw, iters=10):
-    """Config 4: one MoE layer over 4096 tokens, Zipf(1.1)-skewed routing,
-    timed eagerly (one moe_block call per layer) and as replays of a captured
-    graph of one layer."""
-    x = probe.synth_normal(gpu, P_T * P_H, 6060)
-    out = gpu.zeros(P_T * P_H)
-    ws = gpu.zeros(bw.workspace_elems(P_T))
-    bias = gpu.upload(zipf_bias(P_T, P_E, 4))
-    ids = gpu.zeros(P_T * P_K)
+def bench_prefill(gpu, bw, iters=10, T=P_T, flops=PREFILL_FLOPS, bias_np=None, workload=None):
+    """One MoE layer over T tokens (default: config 4, Zipf(1.1)-skewed
+    routing), timed eagerly (one moe_block call per layer) and as replays of
+    a captured graph of one layer; per-kernel times from a held batch."""
+    h, E, K = bw.hidden, bw.experts, bw.k
+    if bias_np is None:
+        bias_np = zipf_bias(T, E, 4)
+    x = probe.synth_normal(gpu, T * h, 6060)
+    out = gpu.zeros(T * h)
+    ws = gpu.zeros(bw.workspace_elems(T))
+    bias = gpu.upload(bias_np)
+    ids = gpu.zeros(T * K)
     for _ in range(2):
         with gpu.batch() as b:
-            b.moe_block(bw, x, out, P_T, ws, logit_bias=bias, ids_out=ids)
+            b.moe_block(bw, x, out, T, ws, logit_bias=bias, ids_out=ids)
     gpu.profile_reset()
     gpu.profile(True)
     with gpu.batch() as b:
         b.hold(HOLD_US)  # every launch queued before the GPU starts: events time GPU work only
-        b.moe_block(bw, x, out, P_T, ws, logit_bias=bias, ids_out=ids)
+        b.moe_block(bw, x, out, T, ws, logit_bias=bias, ids_out=ids)
     prof = gpu.profile_read()
     gpu.profile(False)
     with gpu.batch() as b:
         for _ in range(iters):
-            b.moe_block(bw, x, out, P_T, ws, logit_bias=bias, ids_out=ids)
+            b.moe_block(bw, x, out, T, ws, logit_bias=bias, ids_out=ids)
     t_eager = b.seconds / iters
     cap = gpu.capture()
     with cap as b:
-        b.moe_block(bw, x, out, P_T, ws, logit_bias=bias, ids_out=ids)
+        b.moe_block(bw, x, out, T, ws, logit_bias=bias, ids_out=ids)
     with gpu.batch() as b:
         b.graph(cap.graph)
     with gpu.batch() as b:
         for _ in range(iters):
             b.graph(cap.graph)
     t = b.seconds / iters
-    counts = np.bincount(gpu.read_u32(ids), minlength=P_E)
+    counts = np.bincount(gpu.read_u32(ids), minlength=E)
     k_us = {k: round(v[1] / v[0] * 1e6, 2) for k, v in prof.items()}
     expert_s = sum(v[1] / v[0] for k, v in prof.items() if k in ("gemm_gateup", "gemm_down"))
+    routed_flops = 2 * T * K * 3 * h * bw.keep[1].dims[1]
     for buf in (x, out, ws, bias, ids):
         gpu.release(buf)
     return {
-        "workload": "config4: Qwen3-30B-A3B MoE layer prefill, 4096 tokens (h2048 E128 top8 "
-                    "ff768, 4-bit g64 bf16 quantized from N(0,0.02), Zipf(1.1) router skew), "
-                    "F32 router product, bf16 MFMA expert products",
+        "workload": workload or ("config4: Qwen3-30B-A3B MoE layer prefill, 4096 tokens (h2048 E128 top8 "
+                                 "ff768, 4-bit g64 bf16 quantized from N(0,0.02), Zipf(1.1) router skew), "
+                                 "F32 router product, bf16 MFMA expert products"),
         "expert_weights": "MFMA tile-order copies (moe_pack_weight)" if bw.packed else "row-major",
-        "tokens_per_s": round(P_T / t, 1),
+        "tokens_per_s": round(T / t, 1),
         "ms_per_layer": round(t * 1e3, 4),
         "timing": "graph replay of one layer (hipEvents over 10 replays)",
         "eager_ms_per_layer": round(t_eager * 1e3, 4),
-        "expert_flops": PREFILL_FLOPS,
-        "achieved_TFLOPs": round(PREFILL_FLOPS / t / 1e12, 2),
-        "mfma_frac": round(PREFILL_FLOPS / t / MFMA_PEAK, 4),
-        "expert_kernels_TFLOPs": round(PREFILL_FLOPS / expert_s / 1e12, 2) if expert_s else None,
-        "expert_kernels_mfma_frac": round(PREFILL_FLOPS / expert_s / MFMA_PEAK, 4) if expert_s else None,
+        "expert_flops": flops,
+        "achieved_TFLOPs": round(flops / t / 1e12, 2),
+        "mfma_frac": round(flops / t / MFMA_PEAK, 4),
+        "routed_expert_kernels_TFLOPs": round(routed_flops / expert_s / 1e12, 2) if expert_s else None,
+        "routed_expert_kernels_mfma_frac": round(routed_flops / expert_s / MFMA_PEAK, 4) if expert_s else None,
         "kernels_sum_us": round(sum(k_us.values()), 2),
         "segment_max": int(counts.max()), "segment_min": int(counts.min()),
         "kernels_us": k_us,
     }
+
+
+QN_T = 4096
+QN_FLOPS = 2 * QN_T * K * 3 * H * FF + 2 * QN_T * 3 * H * FFS  # routed + shared expert FLOPs
+
+
+def bench_prefill_qwen3next(gpu, layer):
+    """A Qwen3-Next-shaped prefill (config-2 shapes: E 512, top 10, ff 512,
+    shared ff 512, F32 router, 4-bit g64 experts and shared expert) of 4096
+    tokens over layer 0 of the decode leg, with the experts' MFMA tile-order
+    copies: the shared expert runs as one all-token segment of the grouped
+    bf16 GEMM, on the side stream."""
+    bw0, ws0 = layer
+    router, g, u, d = ws0[:4]
+    pk = [gpu.pack_weight(t) for t in (g, u, d)]
+    _, _, _, _, shared, sgate = bw0.keep
+    bw = BlockWeights(router, g, u, d, K, True, shared, sgate, packed=pk)
+    r = bench_prefill(gpu, bw, T=QN_T, flops=QN_FLOPS, bias_np=np.zeros((QN_T, E), np.float32),
+                      workload="Qwen3-Next-shaped MoE layer prefill, 4096 tokens (config-2 shapes: h2048 "
+                               "E512 top10 ff512 + shared ff512, 4-bit g64 bf16 quantized from N(0,0.02), "
+                               "F32 router, no skew), shared expert on the grouped bf16 GEMM")
+    for p_ in pk:
+        for b_ in p_.buffers:
+            gpu.release(b_)
+    return r
 
 
 # ---- config 3: 8-bit g64 router and shared expert, decode at 1/8/32/64 tokens ----
@@ -550,6 +579,10 @@ def main():
         result["prefill"] = bench_prefill(gpu, pre[0])
         log(f"[bench] prefill: {result['prefill']['ms_per_layer']} ms/layer (graph), "
             f"{result['prefill']['eager_ms_per_layer']} ms eager, {result['prefill']['achieved_TFLOPs']} TFLOP/s")
+        result["prefill_qwen3next"] = bench_prefill_qwen3next(gpu, layers[0])
+        log(f"[bench] Qwen3-Next-shaped prefill: {result['prefill_qwen3next']['ms_per_layer']} ms/layer, "
+            f"{result['prefill_qwen3next']['achieved_TFLOPs']} TFLOP/s, kernels "
+            f"{result['prefill_qwen3next']['kernels_us']}")
     if not args.no_batched:
         c3 = c3_layers(gpu, layers)
         result["batched"] = []

@@ -1,19 +1,21 @@
-// Router product of the prefill path in F32 on the F32 matrix cores
-// (v_mfma_f32_32x32x2_f32): logits[t, e] = x_t . R_e (+ bias), the reference's
-// Batch::matmul(router) (crates/model-runtime/src/execute.rs:220), which
-// multiplies many tokens in F32 (affine_mm / gemm_simd with float 8x8
-// tiles, crates/metal-backend/src/apple/ops/matrix.rs:77-123).
-//
-// The routing is exact given the logits, so the logits themselves must be F32
-// products: bf16 operands change the selected experts of about 1-2% of the
-// tokens of a 4096-token prefill.  Here both operands stay F32: x as stored
-// (or RMS-normalised, F32), and the router's weights decoded to F32 exactly
+// F32 products on the F32 matrix cores (v_mfma_f32_32x32x2_f32):
+// y[t, r] = x_t . W_r (+ bias), W dims [in, out] (dense F32/F16/BF16 or
+// affine 2/4/8-bit).  Two callers:
+//  - the router product of the prefill path, Batch::matmul(router)
+//    (crates/model-runtime/src/execute.rs:220).  The routing is exact given
+//    the logits, so the logits themselves must be F32 products: bf16
+//    operands change the selected experts of about 1-2% of the tokens of a
+//    4096-token prefill;
+//  - moe_matmul at 4 tokens or more, where the reference switches from its
+//    GEMV kernels to tiled F32 GEMMs (affine_mm, gemm_simd / gemm_simd_wide,
+//    crates/metal-backend/src/apple/ops/matrix.rs:77-123).
+// Both operands stay F32: x as given, and the weights decoded to F32 exactly
 // as Tensor::decode does (w = code * scale + bias, one product and one sum,
 // crates/model-format/src/checkpoint.rs:164-196; F16/BF16 widened exactly).
 // The products are the oracle's; only the summation order differs.
 //
 // Block = kWaves waves; wave w owns the 32x32 tile of 32 tokens x experts
-// e0 + 32w .. +31, over one of `ksplit` K ranges, in iterations of 64 K
+// e0 + 32w .. +31 (rows r of W), over one of `ksplit` K ranges, in iterations of 64 K
 // values.  The block's 32 token rows of an iteration reach LDS through
 // coalesced loads (8 threads per 128-byte row segment), shared by the four
 // waves; each lane loads its own expert row's 32 weight values of the
@@ -29,7 +31,7 @@
 
 namespace moehip {
 
-namespace rtr {
+namespace f32mm {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -104,7 +106,7 @@ __device__ __forceinline__ void decode_w(const WRaw<BITS, T> &o, int j, float *v
 }
 
 template <int BITS, int T>
-__global__ __launch_bounds__(kThreads) void router_f32_kernel(WDesc r, const float *__restrict__ x,
+__global__ __launch_bounds__(kThreads) void f32mm_kernel(WDesc r, const float *__restrict__ x,
                                                               uint32_t tokens, uint32_t ksplit,
                                                               const float *__restrict__ bias,
                                                               float *__restrict__ out) {
@@ -198,6 +200,7 @@ __global__ __launch_bounds__(kThreads) void router_f32_kernel(WDesc r, const flo
 struct Launch {
     Prof *p;
     hipStream_t s;
+    const char *name;
     const WDesc &r;
     const float *x;
     uint32_t tokens, ksplit;
@@ -206,38 +209,38 @@ struct Launch {
     template <int BITS, int T>
     hipError_t operator()() {
         const dim3 grid((tokens + 31) / 32, (r.out + 32 * kWaves - 1) / (32 * kWaves), ksplit);
-        return launch_kernel(p, "router_f32", router_f32_kernel<BITS, T>, grid, dim3(kThreads), 0, s, r, x,
-                             tokens, ksplit, bias, out);
+        return launch_kernel(p, name, f32mm_kernel<BITS, T>, grid, dim3(kThreads), 0, s, r, x, tokens, ksplit,
+                             bias, out);
     }
 };
 
-}  // namespace rtr
+}  // namespace f32mm
 
-bool router_f32_supported(const WDesc &r, const float *x) {
+bool f32mm_supported(const WDesc &r, const float *x) {
     const bool kind = r.bits == 0 ? (r.type == 0 || r.type == 1 || r.type == 30)
                                   : (r.bits == 2 || r.bits == 4 || r.bits == 8) &&
                                         (r.type == 0 || r.type == 1 || r.type == 30);
     // an even number of iterations per K range; 16-byte operand loads (rows
     // of a multiple of 128 values start 16-byte aligned)
-    return kind && r.in % (2 * rtr::kIter) == 0 && r.experts == 1 &&
+    return kind && r.in % (2 * f32mm::kIter) == 0 && r.experts == 1 &&
            ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(r.data)) & 15u) == 0;
 }
 
-uint32_t router_f32_ksplit(const WDesc &r, uint32_t tokens, uint64_t part_floats) {
+uint32_t f32mm_ksplit(const WDesc &r, uint32_t tokens, uint64_t part_floats) {
     const uint64_t waves = (uint64_t)((tokens + 31) / 32) * ((r.out + 31) / 32);
     uint32_t ks = 1;
     // K ranges of an even number of iterations, until the grid holds
     // kTargetWaves waves, while the partial sums fit their buffer
-    while (ks < 16 && waves * ks < rtr::kTargetWaves && r.in % (2 * ks * 2 * rtr::kIter) == 0 &&
+    while (ks < 16 && waves * ks < f32mm::kTargetWaves && r.in % (2 * ks * 2 * f32mm::kIter) == 0 &&
            (uint64_t)(2 * ks) * tokens * r.out <= part_floats)
         ks *= 2;
     return ks;
 }
 
-hipError_t launch_router_f32(Prof *p, hipStream_t s, const WDesc &r, const float *x, uint32_t tokens,
-                             uint32_t ksplit, const float *bias, float *out) {
-    if (tokens == 0 || ksplit == 0 || r.in % (ksplit * 2 * rtr::kIter)) return hipErrorInvalidValue;
-    return dispatch_kind(r, rtr::Launch{p, s, r, x, tokens, ksplit, bias, out});
+hipError_t launch_f32mm(Prof *p, hipStream_t s, const char *name, const WDesc &r, const float *x,
+                        uint32_t tokens, uint32_t ksplit, const float *bias, float *out) {
+    if (tokens == 0 || ksplit == 0 || r.in % (ksplit * 2 * f32mm::kIter)) return hipErrorInvalidValue;
+    return dispatch_kind(r, f32mm::Launch{p, s, name, r, x, tokens, ksplit, bias, out});
 }
 
 }  // namespace moehip

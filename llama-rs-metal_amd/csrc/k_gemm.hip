@@ -8,7 +8,7 @@
 //   GATEUP  act[p, j] = silu(x_t . G_e[j]) * (x_t . U_e[j])   t = perm[p] / K
 //           (activation, crates/metal-backend/src/shaders/elementwise.metal:8-17)
 //   DOWN    y[p, r]   = act_p . D_e[r]   (the combine applies the routing weights)
-// (The router product stays F32: k_router.hip.)
+// (The router product stays F32: k_f32mm.hip.)
 //
 // Work item = kTM pairs of one expert x one N-tile (128 weight rows for
 // grouped_gemm, 64 per wave for affine_gemm) over the full K.
@@ -119,7 +119,7 @@ __device__ __forceinline__ void codes_f32(uint32_t w, float *c) {
 struct Args {
     WDesc w, w2;               // B weights (w2: up for GATEUP)
     const uint16_t *a_rows;    // GATEUP: xb16 [T, in]; DOWN: act16 [P, in]
-    const uint32_t *perm;      // pair order (GATEUP: token = perm / k; DOWN: routing weight index)
+    const uint32_t *perm;      // pair order (GATEUP: token = perm / k; null: pair p is row p)
     const uint32_t *offsets;   // [E+1] segment offsets
     const uint32_t *tiles;     // [2*max_tiles] (expert, first position)
     const uint32_t *ntiles;    // number of valid M-tiles (device)
@@ -260,7 +260,7 @@ __global__ __launch_bounds__(kThreads, kBlocksPerCu) void grouped_gemm_kernel(Ar
         for (int i = 0; i < kAChunks; i++) {
             uint32_t pos = m0 + ar + kARowsPerPass * i;
             if (pos >= seg_end) pos = m0;
-            const uint64_t src = MODE == GATEUP ? a.perm[pos] / a.k : pos;
+            const uint64_t src = MODE == GATEUP && a.perm ? a.perm[pos] / a.k : pos;
             asrc[i] = a.a_rows + src * in + 8 * ac;
         }
         // B row of this thread (rows past `out` read row 0 of the expert:
@@ -437,6 +437,11 @@ __device__ __forceinline__ void codes8(const uint32_t *w, int j, float *c) {
 // step j to both operands.  GS = log2(group size) for 16-bit scales, whose
 // scale and bias loads then cover two K steps; 0 for F32 scales (one load
 // per step).
+template <int MODE, int NS>
+__device__ __forceinline__ void affine_store(const Args &a, const f32x16 (&acc)[NS][kAfNT], uint32_t nt,
+                                             uint32_t m0, uint32_t seg_end, uint32_t out, int h, int l32,
+                                             int wv);
+
 template <int MODE, int BITS, int T, int NS, int GS, bool PK>
 __device__ __forceinline__ void affine_item(const Args &a, uint8_t *abuf, uint32_t nt, uint32_t e,
                                             uint32_t m0, uint32_t seg_end, int lane, int wv) {
@@ -455,7 +460,7 @@ __device__ __forceinline__ void affine_item(const Args &a, uint8_t *abuf, uint32
         const uint32_t r = 8 * kAfWaves * i + drow;
         uint32_t pos = m0 + r;
         if (pos >= seg_end) pos = m0;
-        const uint32_t src = MODE == GATEUP ? a.perm[pos] / a.k : pos;
+        const uint32_t src = MODE == GATEUP && a.perm ? a.perm[pos] / a.k : pos;
         aoff[i] = src * in * 2 + (a_chunk(r, dpos) << 4);
     }
     // B: weight row n of tile t; rows past `out` read row 0 (never stored)
@@ -620,10 +625,52 @@ __device__ __forceinline__ void affine_item(const Args &a, uint8_t *abuf, uint32
     // visible and retires both waves' reads of the other stage, which the
     // DMA for kb + 1 then refills.  Past the last step the loads repeat step
     // nk - 1 into the idle stage.
-    AfStage<BITS> bs0, bs1;
-    AfScales sb;
     __builtin_amdgcn_s_waitcnt(0);  // the previous item's last DMA landed
     __builtin_amdgcn_s_barrier();   // and both waves finished reading both stages
+    if (MODE == DOWN && BITS == 4 && nk % 4 == 0) {
+        // (The down product only: config 4 same-box A/B, down 159.8 -> 151.8 us;
+        // gate/up 254.7 -> 262.3 us, so it keeps the one-step loop below.  With
+        // 8-bit codes the fourth stage spills.)
+        // Weights two steps ahead: a ring of four register stages (step kb in
+        // stage kb % 4) and two scale pairs (steps 2p, 2p + 1 in pair p % 2).
+        // Step kb: wait only for this wave's DMA of A step kb (issued one step
+        // earlier; the weight and scale loads issued after it may stay in
+        // flight), barrier, DMA of step kb + 1, weights of kb + 2 and on even
+        // steps the scales of pair kb / 2 + 1, then the MFMAs of step kb.  The
+        // compiler's own waits cover the register stages.
+        constexpr int NB = kAfNT * (BITS == 8 ? 2 : 1) + (GS == 0 ? 2 * kAfNT : 0);  // loads per load_b
+        constexpr int NSB = GS == 0 ? 0 : 2 * kAfNT;                                 // loads per load_sb
+        AfStage<BITS> b4[4];
+        AfScales s2[2];
+        dma(0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_b(b4[0], 0);
+        load_sb(s2[0], 0);
+        load_b(b4[1], 1);
+        auto step = [&](uint32_t kb, auto qc) __attribute__((always_inline)) {
+            constexpr int Q = decltype(qc)::value;  // kb % 4
+            constexpr int N = NB + (Q & 1 ? NSB : 0);  // loads issued after this step's DMA
+            // s_waitcnt vmcnt(N), expcnt and lgkmcnt untouched (gfx9 encoding)
+            __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+            __builtin_amdgcn_s_barrier();
+            dma((Q + 1) & 1, min(kb + 1, nk - 1));
+            // the DMA issues before the loads the wait count above leaves in flight
+            __builtin_amdgcn_sched_barrier(0);
+            load_b(b4[(Q + 2) & 3], min(kb + 2, nk - 1));
+            if constexpr ((Q & 1) == 0) load_sb(s2[((Q >> 1) + 1) & 1], min(kb + 2, nk - 2));
+            compute(abuf + (Q & 1) * kAfATile, b4[Q], s2[(Q >> 1) & 1], Q & 1, kb & ~1u);
+        };
+        for (uint32_t kb = 0; kb < nk; kb += 4) {
+            step(kb, std::integral_constant<int, 0>{});
+            step(kb + 1, std::integral_constant<int, 1>{});
+            step(kb + 2, std::integral_constant<int, 2>{});
+            step(kb + 3, std::integral_constant<int, 3>{});
+        }
+        affine_store<MODE>(a, acc, nt, m0, seg_end, out, h, l32, wv);
+        return;
+    }
+    AfStage<BITS> bs0, bs1;
+    AfScales sb;
     dma(0, 0);
     load_b(bs0, 0);
     load_sb(sb, 0);
@@ -645,7 +692,14 @@ __device__ __forceinline__ void affine_item(const Args &a, uint8_t *abuf, uint32
         load_sb(sb, min(kb + 2, nk - 2));
         compute(abuf + kAfATile, bs1, cur, 1, kb);
     }
-    // acc[s][t][r] = C[32 s + 8 (r / 4) + 4 h + r % 4][this wave's column 32 t + l32]
+    affine_store<MODE>(a, acc, nt, m0, seg_end, out, h, l32, wv);
+}
+
+// acc[s][t][r] = C[32 s + 8 (r / 4) + 4 h + r % 4][this wave's column 32 t + l32]
+template <int MODE, int NS>
+__device__ __forceinline__ void affine_store(const Args &a, const f32x16 (&acc)[NS][kAfNT], uint32_t nt,
+                                             uint32_t m0, uint32_t seg_end, uint32_t out, int h, int l32,
+                                             int wv) {
 #pragma unroll
     for (int s = 0; s < NS; s++) {
 #pragma unroll
@@ -723,9 +777,9 @@ struct Launch {
     uint32_t blocks;
     bool affine;  // affine_gemm_kernel (affine_blocks blocks)
     uint32_t affine_blocks;
+    const char *name;
     template <int BITS, int T>
     hipError_t operator()() {
-        const char *name = MODE == DOWN ? "gemm_down" : "gemm_gateup";
         if constexpr (BITS != 0) {
             if (affine)
                 return launch_kernel(p, name, affine_gemm_kernel<MODE, BITS, T>, dim3(affine_blocks),
@@ -777,7 +831,8 @@ hipError_t launch_grouped_gemm(Prof *p, hipStream_t s, int down, const WDesc &w,
                                const PackedW &pk, const PackedW &pk2, const uint16_t *a_rows,
                                uint64_t a_rows_n, const uint32_t *perm, const uint32_t *offsets,
                                const uint32_t *tiles, const uint32_t *ntiles, uint32_t k,
-                               uint16_t *out) {
+                               uint16_t *out, const char *name) {
+    if (!name) name = down ? "gemm_down" : "gemm_gateup";
     gemm::Args a{};
     a.w = w;
     a.w2 = w2;
@@ -801,11 +856,11 @@ hipError_t launch_grouped_gemm(Prof *p, hipStream_t s, int down, const WDesc &w,
     if (down) {
         a.n_tiles_n = affine ? (w.out + 64 * gemm::kAfWaves - 1) / (64 * gemm::kAfWaves) : (w.out + gemm::kTN - 1) / gemm::kTN;
         if (!affine && (e = dispatch_kind(w, SetLds<gemm::DOWN>{})) != hipSuccess) return e;
-        e = dispatch_kind(w, gemm::Launch<gemm::DOWN>{p, s, a, blocks, affine, affine_blocks});
+        e = dispatch_kind(w, gemm::Launch<gemm::DOWN>{p, s, a, blocks, affine, affine_blocks, name});
     } else {
         a.n_tiles_n = affine ? (w.out + 32 * gemm::kAfWaves - 1) / (32 * gemm::kAfWaves) : (w.out + gemm::kTN / 2 - 1) / (gemm::kTN / 2);
         if (!affine && (e = dispatch_kind(w, SetLds<gemm::GATEUP>{})) != hipSuccess) return e;
-        e = dispatch_kind(w, gemm::Launch<gemm::GATEUP>{p, s, a, blocks, affine, affine_blocks});
+        e = dispatch_kind(w, gemm::Launch<gemm::GATEUP>{p, s, a, blocks, affine, affine_blocks, name});
     }
     return e;
 }

@@ -27,6 +27,18 @@ __global__ __launch_bounds__(256) void gemv_kernel(WDesc w, const float *__restr
     if (lane == 0) *yo = acc;
 }
 
+// One output row (the shared-expert gate scalar x . w_g, [h] reshaped to
+// [h, 1]): one wave per token, four tokens per block.
+template <int BITS, int T>
+__global__ __launch_bounds__(256) void gemv_row1_kernel(WDesc w, const float *__restrict__ x,
+                                                        float *__restrict__ y, uint32_t tokens) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= tokens) return;
+    const float acc = row_dot_generic<BITS, T>(w, 0, x + (uint64_t)t * w.in, lane);
+    if (lane == 0) y[t] = acc;
+}
+
 struct GemvLaunch {
     Prof *p;
     hipStream_t s;
@@ -39,6 +51,9 @@ struct GemvLaunch {
     uint32_t tokens;
     template <int BITS, int T>
     hipError_t operator()() {
+        if (w.out == 1 && nsel == 1 && w.experts == 1)
+            return launch_kernel(p, "gemv_row1", gemv_row1_kernel<BITS, T>, dim3((tokens + 3) / 4), dim3(256), 0,
+                                 s, w, x, y, tokens);
         dim3 grid((w.out + 3) / 4, nsel, tokens);
         return launch_kernel(p, "gemv_generic", gemv_kernel<BITS, T>, grid, dim3(256), 0, s, w, x, xs,
                              ids, y, tokens);
@@ -50,7 +65,9 @@ hipError_t launch_gemv(Prof *p, hipStream_t s, const WDesc &w, const float *x,
                        uint32_t tokens) {
     if (w.out == 0 || nsel == 0 || tokens == 0) return hipSuccess;
     hipError_t e = hipSuccess;
-    if (nsel == 1) {
+    if (nsel == 1 && w.out == 1 && w.experts == 1) {
+        e = dispatch_kind(w, GemvLaunch{p, s, w, x, x_sel_stride, ids, 1, y, tokens});
+    } else if (nsel == 1) {
         // grid.z is limited to 65535: split long token runs (matmul only).
         for (uint32_t t0 = 0; t0 < tokens && e == hipSuccess; t0 += 65535u) {
             const uint32_t n = tokens - t0 < 65535u ? tokens - t0 : 65535u;

@@ -8,6 +8,7 @@
 //   tile_schedule  segment sizes -> list of (expert, first pair) M-tiles (the
 //                  dispatch kernel writes the same list itself where the
 //                  experts fit its LDS; this kernel serves the other cases)
+//   identity_schedule  one segment of all rows (the shared expert on the grouped GEMM)
 //   combine16      out[t] = sum_k w[t, k] * y[pos(t, k)] (+ shared, + residual)
 
 #include "rowdot.hpp"
@@ -122,11 +123,35 @@ __global__ __launch_bounds__(64) void tile_schedule_kernel(const uint32_t *__res
     if (lane == 0) *ntiles = base;
 }
 
-// out[t, i] = sum_k w[t,k] * y16[pos[t*K+k], i] (+ sh_out[t, i]/(1+exp(-sh_gate[t]))) (+ resid[t, i])
+// The schedule of one segment of all T rows (the shared expert's products
+// on the grouped GEMM): offsets {0, T}, M-tiles (0, tm i), their count.
+__global__ __launch_bounds__(256) void identity_schedule_kernel(uint32_t T, uint32_t tm,
+                                                                uint32_t *__restrict__ offsets,
+                                                                uint32_t *__restrict__ tiles,
+                                                                uint32_t *__restrict__ ntiles) {
+    const uint32_t n = (T + tm - 1) / tm;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        tiles[2 * i] = 0;
+        tiles[2 * i + 1] = i * tm;
+    }
+    if (threadIdx.x == 0) {
+        offsets[0] = 0;
+        offsets[1] = T;
+        *ntiles = n;
+    }
+}
+
+// The shared expert's output element o: F32 (sh_out) or bf16 (sh16).
+__device__ __forceinline__ float shared_value(const float *sh_out, const uint16_t *sh16, uint64_t o) {
+    return sh16 ? __uint_as_float((uint32_t)sh16[o] << 16) : sh_out[o];
+}
+
+// out[t, i] = sum_k w[t,k] * y16[pos[t*K+k], i] (+ sh[t, i]/(1+exp(-sh_gate[t]))) (+ resid[t, i])
 __global__ __launch_bounds__(256) void combine16_kernel(const uint16_t *__restrict__ y16,
                                                         const uint32_t *__restrict__ pos,
                                                         const float *__restrict__ wts,
                                                         uint32_t K, const float *__restrict__ sh_out,
+                                                        const uint16_t *__restrict__ sh16,
                                                         const float *__restrict__ sh_gate,
                                                         const float *__restrict__ resid,
                                                         float *__restrict__ out, uint32_t h) {
@@ -141,10 +166,10 @@ __global__ __launch_bounds__(256) void combine16_kernel(const uint16_t *__restri
             v1 += bf16_hi(w) * wk;
         }
         const uint64_t o = (uint64_t)t * h + i;
-        if (sh_out) {
+        if (sh_out || sh16) {
             const float d = 1.0f + expf(-sh_gate[t]);
-            v0 = v0 + sh_out[o] / d;
-            v1 = v1 + sh_out[o + 1] / d;
+            v0 = v0 + shared_value(sh_out, sh16, o) / d;
+            v1 = v1 + shared_value(sh_out, sh16, o + 1) / d;
         }
         if (resid) {
             v0 = resid[o] + v0;
@@ -195,6 +220,7 @@ __global__ __launch_bounds__(256) void combine16v_kernel(const uint16_t *__restr
                                                          const uint32_t *__restrict__ pos,
                                                          const float *__restrict__ wts, uint32_t K,
                                                          const float *__restrict__ sh_out,
+                                                         const uint16_t *__restrict__ sh16,
                                                          const float *__restrict__ sh_gate,
                                                          const float *__restrict__ resid,
                                                          float *__restrict__ out, uint32_t h) {
@@ -229,7 +255,15 @@ __global__ __launch_bounds__(256) void combine16v_kernel(const uint16_t *__restr
         }
     }
     const uint64_t o = (uint64_t)t * h + i;
-    if (sh_out) {
+    if (sh16) {
+        const float d = 1.0f + expf(-sh_gate[t]);
+        const u32x4m r = *reinterpret_cast<const u32x4m *>(sh16 + o);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            v[2 * q] = v[2 * q] + bf16_lo(r[q]) / d;
+            v[2 * q + 1] = v[2 * q + 1] + bf16_hi(r[q]) / d;
+        }
+    } else if (sh_out) {
         const float d = 1.0f + expf(-sh_gate[t]);
 #pragma unroll
         for (int j = 0; j < 8; j++) v[j] = v[j] + sh_out[o + j] / d;
@@ -244,19 +278,27 @@ __global__ __launch_bounds__(256) void combine16v_kernel(const uint16_t *__restr
 }
 
 hipError_t launch_combine16(Prof *p, hipStream_t s, const uint16_t *y16, const uint32_t *pos,
-                            const float *wts, uint32_t k, const float *sh_out, const float *sh_gate,
-                            const float *resid, float *out, uint32_t tokens, uint32_t h) {
-    const bool vec = h % 8 == 0 && (reinterpret_cast<uintptr_t>(y16) & 15u) == 0 &&
-                     (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
+                            const float *wts, uint32_t k, const float *sh_out, const uint16_t *sh16,
+                            const float *sh_gate, const float *resid, float *out, uint32_t tokens,
+                            uint32_t h) {
+    const bool vec = h % 8 == 0 &&
+                     ((reinterpret_cast<uintptr_t>(y16) | reinterpret_cast<uintptr_t>(out) |
+                       reinterpret_cast<uintptr_t>(sh16)) & 15u) == 0;
     if (vec) {
         const uint32_t threads = h / 8 < 256 ? ((h / 8 + 63) / 64) * 64 : 256;
         dim3 grid((h / 8 + threads - 1) / threads, tokens);
         return launch_kernel(p, "combine16", combine16v_kernel, grid, dim3(threads), 0, s, y16, pos,
-                             wts, k, sh_out, sh_gate, resid, out, h);
+                             wts, k, sh_out, sh16, sh_gate, resid, out, h);
     }
     dim3 grid((h / 2 + 255) / 256, tokens);
     return launch_kernel(p, "combine16", combine16_kernel, grid, dim3(256), 0, s, y16, pos, wts, k,
-                         sh_out, sh_gate, resid, out, h);
+                         sh_out, sh16, sh_gate, resid, out, h);
+}
+
+hipError_t launch_identity_schedule(Prof *p, hipStream_t s, uint32_t rows, uint32_t tm, uint32_t *offsets,
+                                    uint32_t *tiles, uint32_t *ntiles) {
+    return launch_kernel(p, "identity_schedule", identity_schedule_kernel, dim3(1), dim3(256), 0, s, rows,
+                         tm, offsets, tiles, ntiles);
 }
 
 }  // namespace moehip

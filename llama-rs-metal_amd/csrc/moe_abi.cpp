@@ -290,6 +290,12 @@ moe_status moe_matmul(moe_gpu *g, const moe_weight *w, moe_buffer x, moe_buffer 
     reads.push_back(rng(x));
     if ((st = check_alias(g, reads, {rng(y)}, false))) return st;
     WDesc d = wdesc(*w);
+    // 4 tokens or more: a tiled F32 product, as the reference switches to
+    // affine_mm / gemm_simd (matrix.rs:77-123); fewer: one GEMV per token
+    if (tokens >= 4 && f32mm_supported(d, (const float *)x.ptr))
+        return launched(g, launch_f32mm(&g->prof, g->stream, "matmul_f32", d, (const float *)x.ptr,
+                                        (uint32_t)tokens, 1, nullptr, (float *)y.ptr),
+                        "matmul");
     return launched(g, launch_gemv(&g->prof, g->stream, d, (const float *)x.ptr, 0, nullptr, 1,
                                    (float *)y.ptr, (uint32_t)tokens),
                     "matmul");

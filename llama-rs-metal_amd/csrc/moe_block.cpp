@@ -16,7 +16,7 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 struct WsLayout {
     uint64_t logits, ids, weights, counts, offsets, perm, pos, act, yexp, sh_act, sh_up, sh_gate,
-        sh_out, xnorm, gates, ups, eo, proj, sgv, xb16, act16, y16, tiles, ntiles, total;
+        sh_out, xnorm, gates, ups, eo, proj, sgv, xb16, act16, y16, tiles, ntiles, sh_sched, total;
 };
 
 inline uint64_t al64(uint64_t n) { return (n + 63) & ~63ull; }
@@ -53,6 +53,9 @@ WsLayout ws_layout(uint64_t T, uint64_t E, uint64_t K, uint64_t h, uint64_t ff, 
     take(L.y16, (T * K * h + 1) / 2);
     take(L.tiles, 2 * ((T * K + 7) / 8 + E + 1));  // MFMA tiles of 128 pairs, batched runs of 8
     take(L.ntiles, 1);
+    // the shared expert's one-segment schedule on the MFMA path: offsets [2],
+    // M-tiles of 128 rows [2 * ceil(T / 128)], their count
+    take(L.sh_sched, 3 + 2 * ((T + 127) / 128));
     L.total = o;
     return L;
 }
@@ -302,6 +305,15 @@ moe_status run_batched(moe_gpu *g, const moe_block_weights *w, const Dims &d, co
     return MOE_OK;
 }
 
+// The shared expert runs on the grouped bf16 GEMM too when its kinds allow
+// (gate and up of one kind; K of both products a multiple of 128).
+bool shared_mfma_ok(const moe_block_weights *w) {
+    if (!w->has_shared) return false;
+    const WDesc SG = wdesc(w->shared_gate), SU = wdesc(w->shared_up), SD = wdesc(w->shared_down);
+    return gemm_supported(SG) && gemm_supported(SU) && gemm_supported(SD) && SG.bits == SU.bits &&
+           SG.type == SU.type && SG.gshift == SU.gshift;
+}
+
 bool mfma_path_ok(const moe_block_weights *w, const Dims &d) {
     const WDesc G = wdesc(w->gate), U = wdesc(w->up), D = wdesc(w->down);
     return gemm_supported(G) && gemm_supported(U) && gemm_supported(D) && G.bits == U.bits &&
@@ -327,21 +339,56 @@ moe_status run_mfma(moe_gpu *g, const moe_block_weights *w, const Dims &d, const
     float *xn = nw ? ws + L.xnorm : nullptr;
     TRY(launch_to_bf16(p, s, xraw, nw, eps, (uint32_t)T, (uint32_t)d.h, xb16, xn));
     const float *xin = nw ? xn : xraw;  // F32 input of the VALU products
+    // The shared expert needs only the input: on the side stream from here,
+    // alongside the router product, routing and dispatch, joined before the
+    // combine.  Its gate/up and down run on the grouped bf16 GEMM as one
+    // segment of all T rows (bf16 output, as the routed experts'); kinds the
+    // GEMM does not take keep the per-token products.
+    const float *so = nullptr, *sgv = nullptr;
+    const uint16_t *so16 = nullptr;
+    SideFork side{g, s};
+    if (w->has_shared) {
+        float *sgt = ws + L.sh_gate;
+        hipStream_t ss = g->side;
+        TRY(side.fork());
+        if (shared_mfma_ok(w)) {
+            uint32_t *soff = reinterpret_cast<uint32_t *>(ws + L.sh_sched), *stiles = soff + 2;
+            uint32_t *snt = stiles + 2 * ((T + 127) / 128);
+            uint16_t *sact16 = reinterpret_cast<uint16_t *>(ws + L.sh_act);
+            uint16_t *sy16 = reinterpret_cast<uint16_t *>(ws + L.sh_out);
+            const PackedW none{};
+            TRY(launch_identity_schedule(p, ss, (uint32_t)T, gemm_tile_rows(), soff, stiles, snt));
+            TRY(launch_grouped_gemm(p, ss, 0, wdesc(w->shared_gate), wdesc(w->shared_up), none, none, xb16, T,
+                                    nullptr, soff, stiles, snt, 1, sact16, "gemm_shared_gateup"));
+            TRY(launch_grouped_gemm(p, ss, 1, wdesc(w->shared_down), wdesc(w->shared_down), none, none, sact16,
+                                    T, nullptr, soff, stiles, snt, 1, sy16, "gemm_shared_down"));
+            so16 = sy16;
+        } else {
+            float *sg = ws + L.sh_act, *su = ws + L.sh_up, *sout = ws + L.sh_out;
+            TRY(launch_gemv(p, ss, wdesc(w->shared_gate), xin, 0, nullptr, 1, sg, (uint32_t)T));
+            TRY(launch_gemv(p, ss, wdesc(w->shared_up), xin, 0, nullptr, 1, su, (uint32_t)T));
+            TRY(launch_swiglu(p, ss, sg, su, sg, T * d.ffs));
+            TRY(launch_gemv(p, ss, wdesc(w->shared_down), sg, 0, nullptr, 1, sout, (uint32_t)T));
+            so = sout;
+        }
+        TRY(launch_gemv(p, ss, gate_inp_desc(w->shared_gate_inp), xin, 0, nullptr, 1, sgt, (uint32_t)T));
+        sgv = sgt;
+    }
     const WDesc R = wdesc(w->router);
     const float *bias = has(io->logit_bias) ? fp(io->logit_bias) : nullptr;
     // the router product stays F32 (the routing is exact given the logits);
     // only the expert products run in bf16
-    if (router_f32_supported(R, xin)) {
+    if (f32mm_supported(R, xin)) {
         // partial sums of the K ranges staged in y16, free until the down GEMM
         float *parts = reinterpret_cast<float *>(y16);
         const uint64_t part_floats = (uint64_t)T * K * d.h / 2;
-        const uint32_t ks = router_f32_ksplit(R, (uint32_t)T, part_floats);
+        const uint32_t ks = f32mm_ksplit(R, (uint32_t)T, part_floats);
         if (ks > 1) {
-            TRY(launch_router_f32(p, s, R, xin, (uint32_t)T, ks, nullptr, parts));
+            TRY(launch_f32mm(p, s, "router_f32", R, xin, (uint32_t)T, ks, nullptr, parts));
             TRY(launch_route_sum(p, s, parts, ks, bias, E, K, w->normalize ? 1 : 0, (uint32_t)T,
                                  logits, ids, wts));
         } else {
-            TRY(launch_router_f32(p, s, R, xin, (uint32_t)T, 1, bias, logits));
+            TRY(launch_f32mm(p, s, "router_f32", R, xin, (uint32_t)T, 1, bias, logits));
             TRY(launch_route(p, s, logits, E, K, w->normalize ? 1 : 0, (uint32_t)T, ids, wts));
         }
     } else {
@@ -351,27 +398,12 @@ moe_status run_mfma(moe_gpu *g, const moe_block_weights *w, const Dims &d, const
     }
     TRY(launch_dispatch(p, s, ids, (uint32_t)(T * K), E, counts, offsets, perm, pos,
                         gemm_tile_rows(), tiles, ntiles));
-    // the shared expert needs only the input: side stream, joined before the combine
-    const float *so = nullptr, *sgv = nullptr;
-    SideFork side{g, s};
-    if (w->has_shared) {
-        float *sg = ws + L.sh_act, *su = ws + L.sh_up, *sout = ws + L.sh_out, *sgt = ws + L.sh_gate;
-        hipStream_t ss = g->side;
-        TRY(side.fork());
-        TRY(launch_gemv(p, ss, wdesc(w->shared_gate), xin, 0, nullptr, 1, sg, (uint32_t)T));
-        TRY(launch_gemv(p, ss, wdesc(w->shared_up), xin, 0, nullptr, 1, su, (uint32_t)T));
-        TRY(launch_swiglu(p, ss, sg, su, sg, T * d.ffs));
-        TRY(launch_gemv(p, ss, wdesc(w->shared_down), sg, 0, nullptr, 1, sout, (uint32_t)T));
-        TRY(launch_gemv(p, ss, gate_inp_desc(w->shared_gate_inp), xin, 0, nullptr, 1, sgt, (uint32_t)T));
-        so = sout;
-        sgv = sgt;
-    }
     TRY(launch_mfma_experts(p, s, wdesc(w->gate), wdesc(w->up), wdesc(w->down), packed(w->gate_packed),
                             packed(w->up_packed), packed(w->down_packed), xb16, (uint32_t)T, offsets, perm,
                             K, tiles, ntiles, act16, y16));
     TRY(side.join());
-    TRY(launch_combine16(p, s, y16, pos, wts, K, so, sgv, io->residual ? xraw : nullptr, out, (uint32_t)T,
-                         (uint32_t)d.h));
+    TRY(launch_combine16(p, s, y16, pos, wts, K, so, so16, sgv, io->residual ? xraw : nullptr, out,
+                         (uint32_t)T, (uint32_t)d.h));
     return MOE_OK;
 }
 

@@ -85,14 +85,16 @@ hipError_t launch_hold(hipStream_t s, uint32_t microseconds);
 hipError_t launch_route_sum(Prof *p, hipStream_t s, const float *parts, uint32_t nsplit,
                             const float *bias, uint32_t experts, uint32_t k, int normalize,
                             uint32_t tokens, float *logits, uint32_t *ids, float *weights);
-// Router product in F32 on the F32 matrix cores (k_router.hip): K split
-// into `ksplit` ranges (router_f32_ksplit picks it for a partial buffer of
-// `part_floats`); with ksplit 1 `out` receives the logits (+ bias), else the
-// partial sums [ksplit, tokens, E] that launch_route_sum adds.
-bool router_f32_supported(const WDesc &r, const float *x);
-uint32_t router_f32_ksplit(const WDesc &r, uint32_t tokens, uint64_t part_floats);
-hipError_t launch_router_f32(Prof *p, hipStream_t s, const WDesc &r, const float *x, uint32_t tokens,
-                             uint32_t ksplit, const float *bias, float *out);
+// out[t, r] = x_t . W_r in F32 on the F32 matrix cores (k_f32mm.hip; the
+// prefill router product and moe_matmul at >= 4 tokens), W 2-D: K split
+// into `ksplit` ranges (f32mm_ksplit picks it for a partial buffer of
+// `part_floats`); with ksplit 1 `out` receives the products (+ bias), else
+// the partial sums [ksplit, tokens, out] (launch_route_sum adds the
+// router's).  Profiled under `name`.
+bool f32mm_supported(const WDesc &w, const float *x);
+uint32_t f32mm_ksplit(const WDesc &w, uint32_t tokens, uint64_t part_floats);
+hipError_t launch_f32mm(Prof *p, hipStream_t s, const char *name, const WDesc &w, const float *x,
+                        uint32_t tokens, uint32_t ksplit, const float *bias, float *out);
 hipError_t launch_route(Prof *p, hipStream_t s, const float *logits, uint32_t experts, uint32_t k,
                         int normalize, uint32_t tokens, uint32_t *ids, float *weights);
 // With `tiles` it also writes the work list of tm-pair runs that
@@ -173,14 +175,21 @@ hipError_t launch_mfma_experts(Prof *p, hipStream_t s, const WDesc &gate, const 
 bool gemm_supported(const WDesc &w);
 uint32_t gemm_tile_rows();  // pairs per work item (the M-tiles tile_schedule emits)
 // pk, pk2: packed copies of w, w2 (PackedW with null data: none).
+// perm null: pair p is row p of a_rows (one segment of all rows, the shared
+// expert).  `name`: the profile name (null: gemm_gateup / gemm_down).
 hipError_t launch_grouped_gemm(Prof *p, hipStream_t s, int down, const WDesc &w, const WDesc &w2,
                                const PackedW &pk, const PackedW &pk2, const uint16_t *a_rows,
                                uint64_t a_rows_n, const uint32_t *perm, const uint32_t *offsets,
                                const uint32_t *tiles, const uint32_t *ntiles, uint32_t k,
-                               uint16_t *out);
+                               uint16_t *out, const char *name = nullptr);
+// offsets {0, rows}, the M-tiles of tm rows over them, and their count
+hipError_t launch_identity_schedule(Prof *p, hipStream_t s, uint32_t rows, uint32_t tm, uint32_t *offsets,
+                                    uint32_t *tiles, uint32_t *ntiles);
+// the shared expert's output as F32 (sh_out) or bf16 (sh16), or neither
 hipError_t launch_combine16(Prof *p, hipStream_t s, const uint16_t *y16, const uint32_t *pos,
-                            const float *wts, uint32_t k, const float *sh_out, const float *sh_gate,
-                            const float *resid, float *out, uint32_t tokens, uint32_t h);
+                            const float *wts, uint32_t k, const float *sh_out, const uint16_t *sh16,
+                            const float *sh_gate, const float *resid, float *out, uint32_t tokens,
+                            uint32_t h);
 
 // ---- batched decode (k_batched.hip) ----
 // Row products over work entries of at most seg_tokens() input rows: entries

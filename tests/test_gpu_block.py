@@ -711,3 +711,27 @@ def test_config4_routing_matches_oracle_f32_logits(gpu, c4):
     assert (~clear).sum() <= T // 1000
     assert np.array_equal(got[2][clear], ref_ids[clear])
     np.testing.assert_allclose(got[3][clear], ref_w[clear], rtol=1e-5, atol=1e-8)
+
+
+@pytest.mark.parametrize("shared,ffs,on_gemm", [((8, 32, BF16), 256, True), ((4, 64, F16), 256, True),
+                                                (DENSE, 256, True), ((4, 64, BF16), 192, False)])
+def test_mfma_path_shared_expert_kinds(gpu, shared, ffs, on_gemm):
+    """The MFMA path runs the shared expert as one all-token segment of the
+    grouped bf16 GEMM when the GEMM takes its kinds (affine or dense, gate
+    and up alike, K of both products a multiple of 128), and keeps the
+    per-token products otherwise (a shared width of 192); both against the
+    oracle at the bf16 tolerance, with the shared gate and the residual."""
+    print(f"[case] MFMA shared kind={shared} ffs={ffs}", flush=True)
+    kinds = {"router": DENSE, "experts": (4, 64, BF16), "shared": shared, "shared_gate": DENSE}
+    blk = HostBlock(256, 16, 4, 128, ffs, kinds, seed=101, random_experts=True)
+    bw = blk.upload(gpu)
+    T = 300
+    x = synth.normal(5400, T * 256).reshape(T, 256)
+    gpu.profile_reset()
+    gpu.profile(True)
+    got = run_block(gpu, bw, x, T, PATH_MFMA, residual=True)
+    prof = gpu.profile_read()
+    gpu.profile(False)
+    assert ("gemm_shared_gateup" in prof) == on_gemm and ("gemm_shared_down" in prof) == on_gemm, sorted(prof)
+    check_all_ids(blk, got)
+    check_against_oracle(blk, x, got, tokens=range(0, T, 7), tol=BF16_TOL, residual=True)

@@ -27,7 +27,7 @@ def test_affine_gemv_and_prefill_all_layouts(gpu, bits, group, st):
     print(f"[case] affine matmul bits={bits} group={group} st={st}", flush=True)
     t = _pattern_tensor([256, 19], bits, group, st)
     w = gpu.weight_tensor(t)
-    for count in [1, 3, 17]:
+    for count in [1, 3, 4, 17]:
         x = (np.sin(np.arange(256 * count, dtype=np.float32) * np.float32(0.27)) * np.float32(0.1))
         x = x.astype(np.float32)
         xb = gpu.upload(x)
@@ -35,6 +35,59 @@ def test_affine_gemv_and_prefill_all_layouts(gpu, bits, group, st):
         with gpu.batch() as b:
             b.matmul(w, xb, y, count)
         close(gpu.read(y), oracle.matmul(t, x, count))
+
+
+@pytest.mark.parametrize("kind", [("dense", F32), ("dense", BF16), ("dense", F16), (4, 64, BF16),
+                                  (8, 128, F16), (2, 32, F32)])
+@pytest.mark.parametrize("tokens", [4, 17, 64, 4096])
+def test_matmul_tiled_f32_tokens(gpu, kind, tokens):
+    """Batch::matmul at 4 tokens or more runs the tiled F32 product (the
+    reference's affine_mm / gemm_simd switch, matrix.rs:77-123) on the F32
+    matrix cores: every token's row against orc_matmul (affine.rs:46-51
+    tolerance), at the dense projection shape h 2048 -> 512 (the shared
+    expert's gate), for every dtype; below 4 tokens the GEMV runs."""
+    from helpers import make_tensor
+    print(f"[case] tiled matmul kind={kind} tokens={tokens}", flush=True)
+    t = make_tensor([2048, 512], kind, seed=tokens + len(kind))
+    w = gpu.weight_tensor(t)
+    x = synth.normal(7000 + tokens, tokens * 2048).reshape(tokens, 2048)
+    xb, y = gpu.upload(x), gpu.zeros(tokens * 512)
+    gpu.profile_reset()
+    gpu.profile(True)
+    with gpu.batch() as b:
+        b.matmul(w, xb, y, tokens)
+    prof = gpu.profile_read()
+    gpu.profile(False)
+    assert "matmul_f32" in prof, sorted(prof)
+    rows = range(tokens) if tokens <= 64 else list(range(0, tokens, 97)) + [tokens - 1]
+    rows = np.array(list(rows))
+    got = gpu.read(y).reshape(tokens, 512)
+    if tokens <= 64:
+        ref = oracle.matmul(t, x, tokens).reshape(tokens, 512)
+        close(got, ref)
+    else:
+        close(got[rows], oracle.matmul(t, x[rows], len(rows)).reshape(len(rows), 512))
+    for b_ in (xb, y):
+        gpu.release(b_)
+
+
+def test_matmul_unaligned_input_uses_gemv(gpu):
+    """An input view that is not 16-byte aligned keeps the per-token GEMV
+    (the tiled product loads 16-byte vectors), with the same results."""
+    t = _pattern_tensor([256, 40], 4, 64, BF16)
+    w = gpu.weight_tensor(t)
+    T = 8
+    x = synth.normal(7100, T * 256 + 1)
+    xb = gpu.upload(x)
+    y = gpu.zeros(T * 40)
+    gpu.profile_reset()
+    gpu.profile(True)
+    with gpu.batch() as b:
+        b.matmul(w, xb.view(1, T * 256), y, T)
+    prof = gpu.profile_read()
+    gpu.profile(False)
+    assert "matmul_f32" not in prof
+    close(gpu.read(y), oracle.matmul(t, x[1:], T))
 
 
 def test_affine_experts_use_gpu_selected_ids(gpu):
