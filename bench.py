@@ -465,6 +465,8 @@ def main():
     ap.add_argument("--no-stack", action="store_true")
     ap.add_argument("--no-batched", action="store_true")
     ap.add_argument("--no-peaks", action="store_true")
+    ap.add_argument("--long-run", type=int, default=LONG_RUN,
+                    help="steps of the steady-state run reported beside `value` (0: none)")
     ap.add_argument("--traffic-probe", choices=["decode", "prefill", "peaks"], default=None,
                     help="short workload for rocprofv3 --pmc runs (no timing output)")
     args = ap.parse_args()
@@ -528,7 +530,7 @@ def main():
     log(f"[bench] timed {steps} steps: {gpu_s * 1e3:.3f} ms (events), {wall * 1e3:.3f} ms (wall)")
     elapsed = max(gpu_s, 1e-12)
     per_step = elapsed / steps
-    long_s = run_graphs(gpu, issue, LONG_RUN, CHUNK) / LONG_RUN
+    long_s = run_graphs(gpu, issue, args.long_run, CHUNK) / args.long_run if args.long_run > 0 else None
 
     dom = "decode_gateup"
     dom_s = kernels.get(dom)
@@ -565,8 +567,8 @@ def main():
                       "all_bytes_per_token": EXPERT_BYTES_PER_TOKEN + ROUTER_BYTES,
                       "achieved_GBps": round(layer_gbps, 1),
                       "frac": round(layer_gbps * 1e9 / HBM_PEAK, 4)},
-        "long_run": {"steps": LONG_RUN, "ms_per_step": round(long_s * 1e3, 6),
-                     "tokens_per_s": round(1.0 / long_s, 1)},
+        "long_run": {"steps": args.long_run, "ms_per_step": round(long_s * 1e3, 6),
+                     "tokens_per_s": round(1.0 / long_s, 1)} if long_s else None,
         "eager_ms_per_step": round(eager_s * 1e3, 6),
         "kernels_us": {k: round(v * 1e6, 3) for k, v in kernels.items()},
         "roofline": roof,
