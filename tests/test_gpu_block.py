@@ -205,16 +205,45 @@ def test_config2_graph_replay(gpu, c2):
         run_block(gpu, bw, synth.normal(1400 + i, 2048).reshape(1, -1), 1)  # eager work between
 
 
+def profiled(gpu, fn):
+    gpu.profile_reset()
+    gpu.profile(True)
+    res = fn()
+    prof = gpu.profile_read()
+    gpu.profile(False)
+    return res, prof
+
+
 def test_profiling_names_kernels(gpu, c2):
     blk, bw = c2
     x = synth.normal(1500, 2048).reshape(1, 2048)
-    gpu.profile_reset()
-    gpu.profile(True)
-    run_block(gpu, bw, x, 1, PATH_AUTO)
-    prof = gpu.profile_read()
-    gpu.profile(False)
+    _, prof = profiled(gpu, lambda: run_block(gpu, bw, x, 1, PATH_AUTO))
     for k in ("decode_pre", "decode_gateup", "decode_down"):
         assert k in prof and prof[k][0] == 1 and prof[k][1] > 0
+
+
+def test_config2_decode_replays_follow_their_inputs(gpu, c2):
+    """40 graph replays of the fused decode over 8 inputs written between the
+    replays (every replay's routing and activations differ from the previous
+    one's): each output equals the eager call on its input and is finite."""
+    blk, bw = c2
+    xs = [synth.normal(1600 + i, 2048) for i in range(8)]
+    eager = [run_block(gpu, bw, x.reshape(1, -1), 1, PATH_AUTO)[0].ravel() for x in xs]
+    xb = gpu.zeros(2048)
+    out = gpu.zeros(2048)
+    ws = gpu.zeros(bw.workspace_elems(1))
+    cap = gpu.capture()
+    with cap as b:
+        b.moe_block(bw, xb, out, 1, ws)
+    for i in range(40):
+        gpu.write(xb, xs[i % 8])
+        with gpu.batch() as b:
+            b.graph(cap.graph)
+        got = gpu.read(out)
+        assert np.all(np.isfinite(got)), i
+        assert np.array_equal(got, eager[i % 8]), i
+    for buf in (xb, out, ws):
+        gpu.release(buf)
 
 
 # ------------------------------------------------------------------ config 3 --
@@ -311,6 +340,24 @@ def test_decode_long_down_rows(gpu, shared):
         ref = run_block(gpu, bw, x, 1, PATH_GROUPED)
         assert np.array_equal(got[2], ref[2])
         assert rel_max_err(got[0], ref[0]) <= F32_TOL
+
+
+@pytest.mark.parametrize("E,shared", [(1100, 0), (1100, 128)])
+def test_decode_many_experts(gpu, E, shared):
+    """The fused decode past 1024 experts, where every routing wave keeps the
+    logits in its LDS: ids, weights and output against the oracle and the
+    grouped path."""
+    print(f"[case] decode E={E} shared={shared}", flush=True)
+    kinds = {"router": DENSE, "experts": (4, 64, BF16), "shared": (4, 64, BF16), "shared_gate": DENSE}
+    blk = HostBlock(256, E, 8, 128, shared, kinds, seed=96 + (shared > 0), random_experts=True)
+    bw = blk.upload(gpu)
+    x = synth.normal(5150 + shared, 256).reshape(1, 256)
+    got, prof = profiled(gpu, lambda: run_block(gpu, bw, x, 1, PATH_AUTO))
+    assert all(k in prof for k in ("decode_pre", "decode_gateup", "decode_down")), sorted(prof)
+    check_against_oracle(blk, x, got)
+    ref = run_block(gpu, bw, x, 1, PATH_GROUPED)
+    assert np.array_equal(got[2], ref[2])
+    assert rel_max_err(got[0], ref[0]) <= F32_TOL
 
 
 @pytest.mark.parametrize("E,K,normalize,ffs", [(64, 1, True, 128), (32, 32, False, 0), (100, 7, False, 128)])
