@@ -4,6 +4,10 @@ Every translation unit under csrc/ is compiled in parallel into _build/ and
 linked into llama-rs-metal_amd/libmoe_hip.so (in-tree, so it travels with the
 repository snapshot to the GPU box); probe/ (the benchmark's measurement
 and synthetic-weight helpers) becomes libmoe_probe.so.  Always rebuilds.
+
+`--timeline` builds the measurement variant libmoe_hip_timeline.so instead:
+the same sources with MOE_TIMELINE defined, so the decode kernels record
+per-wave phase stamps (decode_timeline.py reads them).
 """
 import concurrent.futures as cf
 import glob
@@ -16,6 +20,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmoe_hip.so")
+TIMELINE_BUILD = os.path.join(HERE, "_build_timeline")
+TIMELINE_LIB = os.path.join(HERE, "libmoe_hip_timeline.so")
 PROBE = os.path.join(HERE, "probe")
 PROBE_LIB = os.path.join(HERE, "libmoe_probe.so")
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
@@ -33,9 +39,9 @@ FLAGS = [
 ]
 
 
-def _compile(src):
-    obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, "-x", "hip", "-c", src, "-o", obj]
+def _compile(src, out_dir=BUILD, extra=()):
+    obj = os.path.join(out_dir, os.path.basename(src) + ".o")
+    cmd = [HIPCC, *FLAGS, *extra, "-x", "hip", "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     msgs = "\n".join(l for l in (r.stdout + r.stderr).splitlines()
                      if "packed-fp32-ops" not in l)
@@ -72,5 +78,18 @@ def build(verbose=False):
     return LIB
 
 
+def build_timeline():
+    """Compiles csrc/ with MOE_TIMELINE into libmoe_hip_timeline.so."""
+    os.makedirs(TIMELINE_BUILD, exist_ok=True)
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.cpp")))
+    with cf.ThreadPoolExecutor(max(1, min(8, os.cpu_count() or 1))) as ex:
+        results = list(ex.map(lambda p: _compile(p, TIMELINE_BUILD, ("-DMOE_TIMELINE",)), srcs))
+    _link([o for o, _ in results], TIMELINE_LIB)
+    return TIMELINE_LIB
+
+
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    if "--timeline" in sys.argv:
+        print(build_timeline())
+    else:
+        print(build(verbose="-v" in sys.argv))

@@ -14,6 +14,22 @@
 
 namespace moehip {
 
+// Per-wave phase stamps (s_memrealtime, a 100 MHz clock shared by the whole
+// device) in the measurement build only (build.py --timeline defines
+// MOE_TIMELINE): slot ranges decode_pre [0, 4096), decode_gateup [4096,
+// 10240), decode_down [10240, 16384), eight stamps per slot.  Every lane
+// stores the same value to the same address (no branch around the store, so
+// the measured code is scheduled as in the normal build).
+#ifdef MOE_TIMELINE
+constexpr uint32_t kStampSlots = 16384;
+__device__ uint64_t moe_stamps[kStampSlots * 8];
+#define MOE_STAMP(slot, k) \
+    (moe_stamps[min((uint32_t)(slot), kStampSlots - 1) * 8 + (k)] = __builtin_amdgcn_s_memrealtime())
+#else
+#define MOE_STAMP(slot, k) ((void)0)
+#endif
+constexpr uint32_t kStampPre = 0, kStampGate = 4096, kStampDown = 10240;
+
 struct DecodeKArgs {
     WDesc router, gate, up, down, sg, su, sd, sgi;
     uint32_t has_shared, k, normalize;
@@ -63,6 +79,7 @@ __global__ __launch_bounds__(64) void decode_pre_kernel(DecodeKArgs a) {
     const int lane = threadIdx.x;
     const uint32_t wave_id = blockIdx.x;
     const uint32_t lpr = a.lpr_h, sub = lane / lpr, cl = lane % lpr;
+    MOE_STAMP(kStampPre + wave_id, 0);
     XChunk X;
     X.load(a.x, a.norm_w, cl);
     if (wave_id < a.n_router_waves) {
@@ -79,6 +96,7 @@ __global__ __launch_bounds__(64) void decode_pre_kernel(DecodeKArgs a) {
             else
                 router_item<0, 30>(a, wave_id, sub, cl, X);
         }
+        MOE_STAMP(kStampPre + wave_id, 1);
         return;
     }
     if (a.has_shared && wave_id == a.n_router_waves) {
@@ -89,6 +107,7 @@ __global__ __launch_bounds__(64) void decode_pre_kernel(DecodeKArgs a) {
         if (sub == 0) v = lane_row_dot_any<ST>(a.sgi, 0, cl, a.h / 32, X.xr, xsum);
         v = subwave_sum(v, (int)lpr);
         if (lane == 0) a.sh_gate[0] = v;
+        MOE_STAMP(kStampPre + wave_id, 1);
     }
 }
 
@@ -133,6 +152,7 @@ __global__ __launch_bounds__(64) void decode_gateup_kernel(DecodeKArgs a) {
     const uint32_t wave_id = blockIdx.x;
     const uint32_t routed_waves = a.k * a.n_gate_waves_per_expert;
     const uint32_t shared_waves = a.has_shared ? a.n_shared_waves : 0u;
+    MOE_STAMP(kStampGate + wave_id, 0);
     XChunk X;
     if (wave_id >= routed_waves + shared_waves) {
         // route (sampling.metal:1-36): all K ids and weights
@@ -142,6 +162,7 @@ __global__ __launch_bounds__(64) void decode_gateup_kernel(DecodeKArgs a) {
             a.ids[lane] = s_ids[lane];
             a.weights[lane] = s_w[lane];
         }
+        MOE_STAMP(kStampGate + wave_id, 4);
         return;
     }
     if (wave_id >= routed_waves) {
@@ -152,6 +173,7 @@ __global__ __launch_bounds__(64) void decode_gateup_kernel(DecodeKArgs a) {
         case 4: shared_item<4, ST>(a, item, sub, cl, X); break;
         default: shared_item<8, ST>(a, item, sub, cl, X); break;
         }
+        MOE_STAMP(kStampGate + wave_id, 4);
         return;
     }
     // the id of this wave's selection pass kk of the same routing; the input
@@ -161,6 +183,7 @@ __global__ __launch_bounds__(64) void decode_gateup_kernel(DecodeKArgs a) {
     const uint32_t item = wave_id % a.n_gate_waves_per_expert;
     const uint32_t e = route_one_id(&route_lds, route_vals, a.logits, a.E, a.k, kk, lane,
                                     [&]() { X.load(a.x, a.norm_w, cl); });  // < E by construction
+    MOE_STAMP(kStampGate + wave_id, 1);
     uint64_t rows[kGateFR];
     bool ok[kGateFR];
 #pragma unroll
@@ -173,11 +196,14 @@ __global__ __launch_bounds__(64) void decode_gateup_kernel(DecodeKArgs a) {
     Lg.load(a.gate, rows, ok, cl, a.h / 32);
     Lu.load(a.up, rows, ok, cl, a.h / 32);
     loads_issued();
+    MOE_STAMP(kStampGate + wave_id, 2);
     const float xsum = X.finish(a.norm_w, a.eps, a.h, (int)lpr);
     float g[kGateFR], u[kGateFR];
     Lg.dot(X.xr, xsum, g);
     Lu.dot(X.xr, xsum, u);
+    MOE_STAMP(kStampGate + wave_id, 3);
     gateup_epilogue(g, u, lane, lpr, rpi, sub, cl, item, a.ff, a.act + (uint64_t)kk * a.ff);
+    MOE_STAMP(kStampGate + wave_id, 4);
 }
 
 // ------------------------------------------------------------------ down --
@@ -247,6 +273,7 @@ __device__ __forceinline__ void down_wave(const DecodeKArgs &a, uint32_t wv, uin
             LaneRows<BITS, ST, kDownFR> L;
             L.load(a.down, rows, ok, cl, C);
             loads_issued();
+            MOE_STAMP(kStampDown + blockIdx.x * nw + wv, 1 + q);
             staged_row<SLOTS>(slot, a.act + (uint64_t)kk * a.ff, a.ff, (int)(threadIdx.x & 63), cl, X.xr);
             L.dot(X.xr, X.finish(nullptr, 0.f, 0, 0), part);
 #pragma unroll
@@ -280,6 +307,8 @@ __global__ __launch_bounds__(64 * kDownMaxWaves) void decode_down_kernel(DecodeK
     const uint32_t rows_per_block = rpi * kDownFR;
     const uint32_t row0 = blockIdx.x * rows_per_block;
     float4 *slot = SLOTS ? dslot + wv * (a.ff / 4) : nullptr;
+    const uint32_t stamp = kStampDown + blockIdx.x * nw + wv;
+    MOE_STAMP(stamp, 0);
     // issued first: needed only after the LDS combine
     const float shared_gate = a.has_shared ? a.sh_gate[0] : 0.f;
     float acc_r[kDownFR], acc_s[kDownFR];
@@ -290,6 +319,7 @@ __global__ __launch_bounds__(64 * kDownMaxWaves) void decode_down_kernel(DecodeK
     case 4: down_wave<BITS, ST, 4, SLOTS>(a, wv, nw, row0, sub, cl, rpi, slot, acc_r, acc_s); break;
     default: down_wave<BITS, ST, 8, SLOTS>(a, wv, nw, row0, sub, cl, rpi, slot, acc_r, acc_s); break;
     }
+    MOE_STAMP(stamp, 3);
     static_assert(kDownFR == 2, "reduce-scatter layout assumes two rows per sub-wave");
     if (lpr >= 16) {
         float r, sh;
@@ -325,6 +355,7 @@ __global__ __launch_bounds__(64 * kDownMaxWaves) void decode_down_kernel(DecodeK
             a.out[row] = v;
         }
     }
+    MOE_STAMP(stamp, 4);
 }
 
 // ------------------------------------------------------------------ host --
@@ -407,3 +438,16 @@ hipError_t launch_decode(Prof *p, hipStream_t s, const DecodeArgs &a) {
 }
 
 }  // namespace moehip
+
+#ifdef MOE_TIMELINE
+// Copies the phase stamps out (the measurement build's only export beyond
+// the C ABI).
+extern "C" int moe_timeline_read(void *dst, size_t bytes) {
+    if (bytes > sizeof(moehip::moe_stamps)) return (int)hipErrorInvalidValue;
+    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(moehip::moe_stamps), bytes, 0, hipMemcpyDeviceToHost);
+}
+extern "C" int moe_timeline_clear(void) {
+    static uint64_t zeros[moehip::kStampSlots * 8];
+    return (int)hipMemcpyToSymbol(HIP_SYMBOL(moehip::moe_stamps), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice);
+}
+#endif
