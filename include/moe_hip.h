@@ -265,12 +265,15 @@ moe_status moe_block_workspace(const moe_block_weights *w, uint64_t tokens, uint
  *   tiles[2*n], ntiles[1]  u32: the work list (expert, first position) of every
  *   run of `tile_pairs_mfma` (bf16 MFMA path) or `tile_pairs_batched` (batched
  *   decode) pairs of the non-empty segments, experts ascending, and its
- *   length n (not written by the VALU grouped path).
+ *   length n (not written by the VALU grouped path);
+ *   xb16[T*h]  bf16 (two per element): the bf16 MFMA path's copy of the
+ *   block input (RMS-normalised when io->norm_weight is given), rounded to
+ *   nearest even.
  * logits/ids/weights hold the routing when the io struct gives no outputs. */
 typedef struct {
     uint64_t logits, ids, weights;
     uint64_t counts, offsets, perm, pos;
-    uint64_t tiles, ntiles;
+    uint64_t tiles, ntiles, xb16;
     uint64_t tile_pairs_mfma, tile_pairs_batched;
     uint64_t total; /* = moe_block_workspace */
 } moe_block_layout;

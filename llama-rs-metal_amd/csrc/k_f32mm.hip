@@ -24,7 +24,10 @@
 // halves (the same permutation of K on both operands).  x and the weights
 // are loaded two iterations ahead, in a loop without branches; one barrier
 // per iteration.  Token and expert rows past the ends are clamped for the
-// loads and not stored.
+// loads and not stored.  With `xb16`, the blocks of the first expert column
+// also store x rounded to bf16 (to nearest even) for the bf16 expert GEMMs,
+// from the same staging registers: every (token, K range) is staged by
+// exactly one of them, so x is read once for both products.
 #include <type_traits>
 
 #include "rowdot.hpp"
@@ -37,6 +40,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
 
 constexpr int kWaves = 4;                // expert tiles of 32 per block
 constexpr int kThreads = 64 * kWaves;
@@ -109,7 +113,8 @@ template <int BITS, int T>
 __global__ __launch_bounds__(kThreads) void f32mm_kernel(WDesc r, const float *__restrict__ x,
                                                               uint32_t tokens, uint32_t ksplit,
                                                               const float *__restrict__ bias,
-                                                              float *__restrict__ out) {
+                                                              float *__restrict__ out,
+                                                              uint16_t *__restrict__ xb16) {
     __shared__ __attribute__((aligned(16))) float xs[2][32 * kRow];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const uint32_t i = lane & 31, hf = lane >> 5;
@@ -131,10 +136,17 @@ __global__ __launch_bounds__(kThreads) void f32mm_kernel(WDesc r, const float *_
         xr[q][0] = xg[it * (kIter / 4)];
         xr[q][1] = xg[it * (kIter / 4) + 8];
     };
-    auto put_x = [&](int q, int buf) __attribute__((always_inline)) {
+    // bf16 copy of x: this thread's 2 x 4 values of iteration `it` of its row
+    const bool copy = xb16 && blockIdx.y == 0 && t0 + srow < tokens;
+    uint16_t *xbrow = copy ? xb16 + (uint64_t)(t0 + srow) * h + kbeg + 4 * sch : nullptr;
+    auto put_x = [&](int q, int buf, uint32_t it) __attribute__((always_inline)) {
         float *d = &xs[buf][srow * kRow + 4 * sch];
         *reinterpret_cast<f32x4 *>(d) = xr[q][0];
         *reinterpret_cast<f32x4 *>(d + 32) = xr[q][1];
+        if (copy && it < iters) {
+            *reinterpret_cast<bf16x4 *>(xbrow + it * kIter) = __builtin_convertvector(xr[q][0], bf16x4);
+            *reinterpret_cast<bf16x4 *>(xbrow + it * kIter + 32) = __builtin_convertvector(xr[q][1], bf16x4);
+        }
     };
     // one iteration: MFMA s of half j multiplies x[i][32hf + 16j + s] with
     // R[e][32hf + 16j + s] (the same permutation of K on both operands)
@@ -159,7 +171,7 @@ __global__ __launch_bounds__(kThreads) void f32mm_kernel(WDesc r, const float *_
     gload_x(1, min(1u, iters - 1));
     load_w<BITS, T>(r, wel, wr[0]);
     load_w<BITS, T>(r, wel + (uint64_t)min(1u, iters - 1) * kIter, wr[1]);
-    put_x(0, 0);
+    put_x(0, 0, 0);
     __syncthreads();
     // Iteration it (stage Q = it % 2): load x of it + 2 into register stage Q
     // (its x of `it` went to LDS one iteration earlier); multiply LDS buffer
@@ -175,7 +187,7 @@ __global__ __launch_bounds__(kThreads) void f32mm_kernel(WDesc r, const float *_
         __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs
         compute(Q, Q);
         load_w<BITS, T>(r, wel + (uint64_t)min(it + 2, iters - 1) * kIter, wr[Q]);
-        put_x(Q ^ 1, Q ^ 1);
+        put_x(Q ^ 1, Q ^ 1, it + 1);  // x of iteration it + 1 (loaded one iteration earlier)
         __syncthreads();
     };
     for (uint32_t it = 0; it < iters; it += 2) {
@@ -206,11 +218,12 @@ struct Launch {
     uint32_t tokens, ksplit;
     const float *bias;
     float *out;
+    uint16_t *xb16;
     template <int BITS, int T>
     hipError_t operator()() {
         const dim3 grid((tokens + 31) / 32, (r.out + 32 * kWaves - 1) / (32 * kWaves), ksplit);
         return launch_kernel(p, name, f32mm_kernel<BITS, T>, grid, dim3(kThreads), 0, s, r, x, tokens, ksplit,
-                             bias, out);
+                             bias, out, xb16);
     }
 };
 
@@ -238,9 +251,9 @@ uint32_t f32mm_ksplit(const WDesc &r, uint32_t tokens, uint64_t part_floats) {
 }
 
 hipError_t launch_f32mm(Prof *p, hipStream_t s, const char *name, const WDesc &r, const float *x,
-                        uint32_t tokens, uint32_t ksplit, const float *bias, float *out) {
+                        uint32_t tokens, uint32_t ksplit, const float *bias, float *out, uint16_t *xb16) {
     if (tokens == 0 || ksplit == 0 || r.in % (ksplit * 2 * f32mm::kIter)) return hipErrorInvalidValue;
-    return dispatch_kind(r, f32mm::Launch{p, s, name, r, x, tokens, ksplit, bias, out});
+    return dispatch_kind(r, f32mm::Launch{p, s, name, r, x, tokens, ksplit, bias, out, xb16});
 }
 
 }  // namespace moehip

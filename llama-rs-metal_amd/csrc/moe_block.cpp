@@ -337,13 +337,46 @@ moe_status run_mfma(moe_gpu *g, const moe_block_weights *w, const Dims &d, const
     uint32_t *tiles = reinterpret_cast<uint32_t *>(ws + L.tiles);
     uint32_t *ntiles = reinterpret_cast<uint32_t *>(ws + L.ntiles);
     float *xn = nw ? ws + L.xnorm : nullptr;
-    TRY(launch_to_bf16(p, s, xraw, nw, eps, (uint32_t)T, (uint32_t)d.h, xb16, xn));
-    const float *xin = nw ? xn : xraw;  // F32 input of the VALU products
+    const float *xin = nw ? xn : xraw;  // F32 input of the router and the VALU products
+    const WDesc R = wdesc(w->router);
+    const float *bias = has(io->logit_bias) ? fp(io->logit_bias) : nullptr;
+    // the router product stays F32 (the routing is exact given the logits);
+    // only the expert products run in bf16.  `x16`: the router also rounds x
+    // to bf16 for them (one pass over x where there is no norm to apply).
+    auto router = [&](uint16_t *x16) -> moe_status {
+        if (f32mm_supported(R, xin)) {
+            // partial sums of the K ranges staged in y16, free until the down GEMM
+            float *parts = reinterpret_cast<float *>(y16);
+            const uint64_t part_floats = (uint64_t)T * K * d.h / 2;
+            const uint32_t ks = f32mm_ksplit(R, (uint32_t)T, part_floats);
+            if (ks > 1) {
+                TRY(launch_f32mm(p, s, "router_f32", R, xin, (uint32_t)T, ks, nullptr, parts, x16));
+                TRY(launch_route_sum(p, s, parts, ks, bias, E, K, w->normalize ? 1 : 0, (uint32_t)T,
+                                     logits, ids, wts));
+            } else {
+                TRY(launch_f32mm(p, s, "router_f32", R, xin, (uint32_t)T, 1, bias, logits, x16));
+                TRY(launch_route(p, s, logits, E, K, w->normalize ? 1 : 0, (uint32_t)T, ids, wts));
+            }
+        } else {
+            TRY(launch_gemv(p, s, R, xin, 0, nullptr, 1, logits, (uint32_t)T));
+            if (bias) TRY(launch_add(p, s, logits, bias, logits, T * d.E));
+            TRY(launch_route(p, s, logits, E, K, w->normalize ? 1 : 0, (uint32_t)T, ids, wts));
+        }
+        return MOE_OK;
+    };
+    const bool router_rounds = !nw && f32mm_supported(R, xin);
+    if (router_rounds) {
+        const moe_status st = router(xb16);
+        if (st != MOE_OK) return st;
+    } else {
+        TRY(launch_to_bf16(p, s, xraw, nw, eps, (uint32_t)T, (uint32_t)d.h, xb16, xn));
+    }
     // The shared expert needs only the input: on the side stream from here,
-    // alongside the router product, routing and dispatch, joined before the
-    // combine.  Its gate/up and down run on the grouped bf16 GEMM as one
-    // segment of all T rows (bf16 output, as the routed experts'); kinds the
-    // GEMM does not take keep the per-token products.
+    // alongside the router product (when that does not produce the bf16
+    // input), routing and dispatch, joined before the combine.  Its gate/up
+    // and down run on the grouped bf16 GEMM as one segment of all T rows
+    // (bf16 output, as the routed experts'); kinds the GEMM does not take keep
+    // the per-token products.
     const float *so = nullptr, *sgv = nullptr;
     const uint16_t *so16 = nullptr;
     SideFork side{g, s};
@@ -374,27 +407,9 @@ moe_status run_mfma(moe_gpu *g, const moe_block_weights *w, const Dims &d, const
         TRY(launch_gemv(p, ss, gate_inp_desc(w->shared_gate_inp), xin, 0, nullptr, 1, sgt, (uint32_t)T));
         sgv = sgt;
     }
-    const WDesc R = wdesc(w->router);
-    const float *bias = has(io->logit_bias) ? fp(io->logit_bias) : nullptr;
-    // the router product stays F32 (the routing is exact given the logits);
-    // only the expert products run in bf16
-    if (f32mm_supported(R, xin)) {
-        // partial sums of the K ranges staged in y16, free until the down GEMM
-        float *parts = reinterpret_cast<float *>(y16);
-        const uint64_t part_floats = (uint64_t)T * K * d.h / 2;
-        const uint32_t ks = f32mm_ksplit(R, (uint32_t)T, part_floats);
-        if (ks > 1) {
-            TRY(launch_f32mm(p, s, "router_f32", R, xin, (uint32_t)T, ks, nullptr, parts));
-            TRY(launch_route_sum(p, s, parts, ks, bias, E, K, w->normalize ? 1 : 0, (uint32_t)T,
-                                 logits, ids, wts));
-        } else {
-            TRY(launch_f32mm(p, s, "router_f32", R, xin, (uint32_t)T, 1, bias, logits));
-            TRY(launch_route(p, s, logits, E, K, w->normalize ? 1 : 0, (uint32_t)T, ids, wts));
-        }
-    } else {
-        TRY(launch_gemv(p, s, R, xin, 0, nullptr, 1, logits, (uint32_t)T));
-        if (bias) TRY(launch_add(p, s, logits, bias, logits, T * d.E));
-        TRY(launch_route(p, s, logits, E, K, w->normalize ? 1 : 0, (uint32_t)T, ids, wts));
+    if (!router_rounds) {
+        const moe_status st = router(nullptr);
+        if (st != MOE_OK) return st;
     }
     TRY(launch_dispatch(p, s, ids, (uint32_t)(T * K), E, counts, offsets, perm, pos,
                         gemm_tile_rows(), tiles, ntiles));
@@ -450,8 +465,8 @@ moe_status moe_block_workspace_layout(const moe_block_weights *w, uint64_t token
     const uint64_t h = w->router.dims[0], E = w->router.dims[1], K = w->experts_used;
     const uint64_t ff = w->gate.dims[1], ffs = w->has_shared ? w->shared_gate.dims[1] : 0;
     const WsLayout L = ws_layout(tokens, E, K, h, ff, ffs);
-    *out = moe_block_layout{L.logits, L.ids,   L.weights, L.counts,         L.offsets,    L.perm,
-                            L.pos,    L.tiles, L.ntiles,  gemm_tile_rows(), seg_tokens(), L.total};
+    *out = moe_block_layout{L.logits, L.ids,   L.weights, L.counts, L.offsets,        L.perm,       L.pos,
+                            L.tiles,  L.ntiles, L.xb16,   gemm_tile_rows(), seg_tokens(), L.total};
     return MOE_OK;
 }
 

@@ -93,8 +93,10 @@ hipError_t launch_route_sum(Prof *p, hipStream_t s, const float *parts, uint32_t
 // router's).  Profiled under `name`.
 bool f32mm_supported(const WDesc &w, const float *x);
 uint32_t f32mm_ksplit(const WDesc &w, uint32_t tokens, uint64_t part_floats);
+// xb16 (optional, [tokens, in]): x rounded to bf16, written on the way.
 hipError_t launch_f32mm(Prof *p, hipStream_t s, const char *name, const WDesc &w, const float *x,
-                        uint32_t tokens, uint32_t ksplit, const float *bias, float *out);
+                        uint32_t tokens, uint32_t ksplit, const float *bias, float *out,
+                        uint16_t *xb16 = nullptr);
 hipError_t launch_route(Prof *p, hipStream_t s, const float *logits, uint32_t experts, uint32_t k,
                         int normalize, uint32_t tokens, uint32_t *ids, float *weights);
 // With `tiles` it also writes the work list of tm-pair runs that

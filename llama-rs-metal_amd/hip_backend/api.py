@@ -104,7 +104,7 @@ class MoeBlockWeightsC(C.Structure):
 
 class MoeBlockLayoutC(C.Structure):
     _fields_ = [(n, C.c_uint64) for n in (
-        "logits", "ids", "weights", "counts", "offsets", "perm", "pos", "tiles", "ntiles",
+        "logits", "ids", "weights", "counts", "offsets", "perm", "pos", "tiles", "ntiles", "xb16",
         "tile_pairs_mfma", "tile_pairs_batched", "total")]
 
 

@@ -115,9 +115,10 @@ def test_pack_size_is_host_only():
 
 
 def test_workspace_layout_is_host_only():
-    """moe_block_workspace_layout: the routing and dispatch regions lie inside
-    the workspace, do not overlap, and are large enough for T tokens; the
-    work-list region holds the largest list either tile size can produce."""
+    """moe_block_workspace_layout: the routing, dispatch and bf16-input
+    regions lie inside the workspace, do not overlap, and are large enough for
+    T tokens; the work-list region holds the largest list either tile size can
+    produce."""
     lib = api.load_library()
     w = api.MoeBlockWeightsC()
     w.router.ndims, w.router.dims[0], w.router.dims[1] = 2, 2048, 128
@@ -134,7 +135,7 @@ def test_workspace_layout_is_host_only():
     worst_tiles = T * K // lay.tile_pairs_batched + E  # one partial run per expert
     spans = sorted([(lay.logits, T * E), (lay.ids, T * K), (lay.weights, T * K), (lay.counts, E),
                     (lay.offsets, E + 1), (lay.perm, T * K), (lay.pos, T * K),
-                    (lay.tiles, 2 * worst_tiles), (lay.ntiles, 1)])
+                    (lay.tiles, 2 * worst_tiles), (lay.ntiles, 1), (lay.xb16, T * 2048 // 2)])
     for (a, na), (b, _) in zip(spans, spans[1:]):
         assert a + na <= b
     assert spans[-1][0] + spans[-1][1] <= lay.total

@@ -730,6 +730,34 @@ def test_grouped_and_mfma_dispatch_in_block(gpu, c4, T):
         check_in_block_dispatch(bw, T, got[2], wsd["ws"], tm=tm)
 
 
+def bf16_rne_bits(v):
+    """float32 -> bf16 bits, rounded to nearest even (no NaNs in the inputs)."""
+    u = np.ascontiguousarray(v, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+@pytest.mark.parametrize("norm", [False, True])
+def test_mfma_bf16_input_copy(gpu, c4, norm):
+    """The bf16 copy of the block input the expert GEMMs multiply: without a
+    norm weight the router product writes it while it stages x; with one, the
+    norm kernel does.  Both bit-exact against round-to-nearest-even of x (of
+    RMSNorm(x) as the oracle computes it, to one bf16 step, with the norm)."""
+    blk, bw = c4
+    T, h = 300, 2048
+    x = synth.normal(6100 + norm, T * h).reshape(T, h)
+    nw = (1.0 + 0.1 * synth.normal(6110, h)).astype(np.float32) if norm else None
+    wsd = {}
+    run_block(gpu, bw, x, T, PATH_MFMA, norm_w=nw, ws_out=wsd)
+    lay = bw.workspace_layout(T)
+    got = wsd["ws"][lay["xb16"]:lay["xb16"] + T * h // 2].view(np.uint16).reshape(T, h)
+    if not norm:
+        assert np.array_equal(got, bf16_rne_bits(x))
+    else:
+        ref = np.stack([oracle.rms_norm(r, nw, 1e-6) for r in x])
+        diff = np.abs(got.astype(np.int32) - bf16_rne_bits(ref).astype(np.int32))
+        assert diff.max() <= 1, diff.max()
+
+
 def test_config4_routing_matches_oracle_f32_logits(gpu, c4):
     """The prefill path routes on F32 router products: its logits of all
     4096 tokens agree with the oracle's own F32 logits (orc_matmul, the
