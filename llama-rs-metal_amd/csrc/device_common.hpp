@@ -67,6 +67,11 @@ constexpr int kDppMirror = 0x140;
 constexpr int kDppRor4 = 0x124;
 constexpr int kDppRor8 = 0x128;
 
+// LDS writes of this wave are complete and visible to its other lanes.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+}
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));

@@ -100,11 +100,6 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
                                      __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
-// LDS writes of this wave are complete and visible to its other lanes.
-__device__ __forceinline__ void wave_lds_sync() {
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-    __builtin_amdgcn_wave_barrier();
-}
 
 // Lane `lane` holds elements j = R*lane + i (i < R): two 16-byte loads per
 // lane when R is a multiple of 4 and the row is aligned and whole.
