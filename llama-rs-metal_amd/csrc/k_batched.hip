@@ -23,6 +23,8 @@
 
 namespace moehip {
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 constexpr uint32_t kSegTokens = 8;  // pairs per work entry over the dispatched segments
 constexpr uint32_t kSegRun = 2;     // input rows per entry over all tokens (router, shared
                                     // expert): small weights, so more waves beat re-reads
@@ -152,27 +154,31 @@ __global__ __launch_bounds__(64) void seg_gateup_kernel(SegArgs a) {
 // (lane l: float4s l, l + 64, ...), written to one of the wave's two LDS
 // slots (float4 i of chunk c at i * C + c) and read back per sub-wave; the
 // next row's loads are in flight while the current row is multiplied.
-template <typename RowOf, typename Body>
+// NPL: float4s per lane when the width is a compile-time multiple of 256
+// (every lane loads the same count, so the loads stay unconditional and in
+// registers; a per-lane bound made the compiler wait on each load and keep
+// the row in scratch); 0 for a run-time width.
+template <int NPL, typename RowOf, typename Body>
 __device__ __forceinline__ void over_inputs_staged(float4 *slots, const float *in, uint32_t width,
                                                    int lane, uint32_t cl, uint32_t beg, uint32_t end,
                                                    RowOf row_of, Body body) {
-    constexpr int kMaxPerLane = 8;  // width <= 2048
+    constexpr int kMaxPerLane = NPL ? NPL : 8;  // width <= 2048
     const uint32_t C = width / 32, n4 = width / 4;
-    float4 nx[kMaxPerLane];
+    f32x4 nx[kMaxPerLane];  // a plain vector type: HIP's float4 struct kept the row in scratch
     auto fetch = [&](uint32_t p) {
-        const float4 *src = reinterpret_cast<const float4 *>(in + (uint64_t)row_of(p) * width);
+        const f32x4 *src = reinterpret_cast<const f32x4 *>(in + (uint64_t)row_of(p) * width);
 #pragma unroll
         for (int j = 0; j < kMaxPerLane; j++)
-            if ((uint32_t)(lane + 64 * j) < n4) nx[j] = src[lane + 64 * j];
+            if (NPL || (uint32_t)(lane + 64 * j) < n4) nx[j] = src[lane + 64 * j];
     };
     fetch(beg);
 #pragma unroll 1
     for (uint32_t p = beg; p < end; p++) {
-        float4 *slot = slots + (p & 1) * n4;
+        f32x4 *slot = reinterpret_cast<f32x4 *>(slots) + (p & 1) * n4;
 #pragma unroll
         for (int j = 0; j < kMaxPerLane; j++) {
             const uint32_t w4 = lane + 64 * j;
-            if (w4 < n4) slot[(w4 % 8) * C + w4 / 8] = nx[j];
+            if (NPL || w4 < n4) slot[(w4 % 8) * C + w4 / 8] = nx[j];
         }
         if (p + 1 < end) fetch(p + 1);
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's slot writes landed
@@ -180,11 +186,11 @@ __device__ __forceinline__ void over_inputs_staged(float4 *slots, const float *i
         InChunk X;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const float4 v = slot[i * C + cl];
-            X.v[4 * i] = v.x;
-            X.v[4 * i + 1] = v.y;
-            X.v[4 * i + 2] = v.z;
-            X.v[4 * i + 3] = v.w;
+            const f32x4 v = slot[i * C + cl];
+            X.v[4 * i] = v[0];
+            X.v[4 * i + 1] = v[1];
+            X.v[4 * i + 2] = v[2];
+            X.v[4 * i + 3] = v[3];
         }
         body(X, p);
     }
@@ -227,7 +233,8 @@ __global__ __launch_bounds__(64) void seg_rows_kernel(SegArgs a) {
         // rows of fewer than 64 lanes (the run-time width is never 64: those
         // rows take LPR 64): the input rows through the wave's LDS slots
         extern __shared__ float4 slots[];  // 2 x in / 4
-        over_inputs_staged(slots, a.in, in, lane, cl, beg, end, [](uint32_t p) { return p; }, body);
+        constexpr int kNpl = LPR * 32 % 256 == 0 ? LPR * 32 / 256 : 0;
+        over_inputs_staged<kNpl>(slots, a.in, in, lane, cl, beg, end, [](uint32_t p) { return p; }, body);
     } else {
         over_inputs(a.in, in, cl, beg, end, [](uint32_t p) { return p; }, body);
     }
