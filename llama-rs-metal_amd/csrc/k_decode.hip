@@ -63,6 +63,12 @@ __device__ __forceinline__ void router_item(const DecodeKArgs &a, uint32_t wave_
     }
     LaneRows<BR, TR, kPreFR> L;
     L.load(a.router, e, ok, cl, a.h / 32);
+    // the logit bias loads with the rows (no bias: a dummy read of x[0]), so
+    // its latency is not added after the products
+    const float *bsrc = a.logit_bias ? a.logit_bias : a.x;
+    float bias[kPreFR];
+#pragma unroll
+    for (int f = 0; f < kPreFR; f++) bias[f] = bsrc[a.logit_bias && ok[f] ? e[f] : 0u];
     loads_issued();
     const float xsum = X.finish(a.norm_w, a.eps, a.h, (int)lpr);
     float v[kPreFR];
@@ -70,7 +76,7 @@ __device__ __forceinline__ void router_item(const DecodeKArgs &a, uint32_t wave_
 #pragma unroll
     for (int f = 0; f < kPreFR; f++) {
         const float r = subwave_sum(v[f], (int)lpr);
-        if (ok[f] && cl == 0) a.logits[e[f]] = a.logit_bias ? r + a.logit_bias[e[f]] : r;
+        if (ok[f] && cl == 0) a.logits[e[f]] = a.logit_bias ? r + bias[f] : r;
     }
 }
 
