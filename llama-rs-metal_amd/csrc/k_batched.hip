@@ -135,15 +135,23 @@ __global__ __launch_bounds__(64) void seg_gateup_kernel(SegArgs a) {
     loads_issued();
     over_inputs(a.in, in, cl, beg, end, [&](uint32_t p) { return a.perm ? a.perm[p] / a.k : p; },
                 [&](const InChunk &X, uint32_t p) {
+                    const float xs = X.sum();
+                    // 4-bit codes: the input's limbs, shared by all the wave's rows
+                    XLimbs xl;
+                    if constexpr (BITS == 4) xl.build(X.v);
 #pragma unroll
                     for (int q = 0; q < kSegGateItems; q++) {
                         Lg[q].pin();
                         Lu[q].pin();
                         const uint32_t item = blockIdx.x * kSegGateItems + q;
-                        const float xs = X.sum();
                         float g[kGateFR], u[kGateFR];
-                        Lg[q].dot(X.v, xs, g);
-                        Lu[q].dot(X.v, xs, u);
+                        if constexpr (BITS == 4) {
+                            Lg[q].dot_limbs(xl, xs, g);
+                            Lu[q].dot_limbs(xl, xs, u);
+                        } else {
+                            Lg[q].dot(X.v, xs, g);
+                            Lu[q].dot(X.v, xs, u);
+                        }
                         gateup_epilogue(g, u, lane, lpr, rpi, sub, cl, item, ff, a.out + (uint64_t)p * ff);
                     }
                 });

@@ -106,6 +106,84 @@ struct LaneRows {
             res[f] = ok[f] ? v : 0.f;
         }
     }
+    // The same products for 4-bit rows from the input's limbs (XLimbs).
+    template <typename XL>
+    __device__ __forceinline__ void dot_limbs(const XL &xl, float xsum, float *res) const {
+        static_assert(BITS == 4, "limb products take 4-bit codes");
+#pragma unroll
+        for (int f = 0; f < R; f++) {
+            const float v = raw_to_f32<T>(sr[f]) * xl.dot4(c[f].w) + raw_to_f32<T>(br[f]) * xsum;
+            res[f] = ok[f] ? v : 0.f;
+        }
+    }
+};
+
+// A lane's 32-element input chunk as six 4-bit limbs, for 4-bit codes on
+// the integer dot-product unit (v_dot8_u32_u4: eight code x limb products
+// per instruction, against one conversion and one FMA per code in
+// Chunk32::dot).  With 2^e > max|x| over the chunk, X_j = round(x_j 2^(22-e))
+// + 2^22 lies in [0, 2^23): the FMA x_j 2^(22-e) + 3 * 2^22 leaves it in the
+// float's mantissa bits (the exponent bit above them is 0 in [2^23, 2^24)).
+// W[l][i] holds nibble l of X_8i .. X_8i+7 in code order, so
+// sum_j c_j X_j = sum_l 16^l udot8(codes, W[l]) exactly; the 2^22 offset is
+// taken off with sum_j c_j.  One rounding of the exact integer sum
+// (2^-23 of the chunk maximum per input, the F32 FMA chain's order of
+// error).  A non-finite input makes the chunk's scale NaN.
+struct XLimbs {
+    uint32_t W[6][4];
+    float scale;  // 2^(e - 22)
+    __device__ __forceinline__ void build(const float *x) {
+        float m = 0.f;
+#pragma unroll
+        for (int j = 0; j < 32; j++) m = fmaxf(m, fabsf(x[j]));
+        const int e = __builtin_amdgcn_frexp_expf(m);
+        const float up = __builtin_amdgcn_ldexpf(1.0f, 22 - e);
+        scale = __builtin_isfinite(m) ? __builtin_amdgcn_ldexpf(1.0f, e - 22) : __builtin_nanf("");
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            uint32_t X[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) X[j] = __float_as_uint(fmaf(x[8 * i + j], up, 12582912.0f));
+            // bytes k of the even (E) and odd (O) elements: E_k = (X0, X2, X4, X6) byte k
+            uint32_t E[3], O[3];
+#pragma unroll
+            for (int par = 0; par < 2; par++) {
+                const uint32_t a = X[par], b = X[par + 2], c = X[par + 4], d = X[par + 6];
+                const uint32_t ab01 = __builtin_amdgcn_perm(b, a, 0x05010400u);  // a0 b0 a1 b1
+                const uint32_t cd01 = __builtin_amdgcn_perm(d, c, 0x05010400u);
+                const uint32_t ab23 = __builtin_amdgcn_perm(b, a, 0x07030602u);  // a2 b2 a3 b3
+                const uint32_t cd23 = __builtin_amdgcn_perm(d, c, 0x07030602u);
+                uint32_t *B = par ? O : E;
+                B[0] = __builtin_amdgcn_perm(cd01, ab01, 0x05040100u);  // a0 b0 c0 d0
+                B[1] = __builtin_amdgcn_perm(cd01, ab01, 0x07060302u);  // a1 b1 c1 d1
+                B[2] = __builtin_amdgcn_perm(cd23, ab23, 0x05040100u);  // a2 b2 c2 d2
+            }
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                // nibble 2n <- element 2n, nibble 2n + 1 <- element 2n + 1
+                W[2 * k][i] = (E[k] & 0x0f0f0f0fu) | ((O[k] << 4) & 0xf0f0f0f0u);
+                W[2 * k + 1][i] = ((E[k] >> 4) & 0x0f0f0f0fu) | (O[k] & 0xf0f0f0f0u);
+            }
+        }
+    }
+    // sum_j c_j x_j for the chunk's 32 4-bit codes (4 words, code j of word i
+    // multiplies element 8i + j)
+    __device__ __forceinline__ float dot4(const uint32_t *w) const {
+        uint32_t P[6];
+#pragma unroll
+        for (int l = 0; l < 6; l++) {
+            uint32_t acc = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_udot8(w[i], W[l][i], acc, false);
+            P[l] = acc;  // <= 32 * 15 * 15
+        }
+        uint32_t cs = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) cs = __builtin_amdgcn_udot8(w[i], 0x11111111u, cs, false);
+        const uint32_t lo = P[0] + (P[1] << 4) + (P[2] << 8);                       // < 2^21
+        const int32_t hi = (int32_t)(P[3] + (P[4] << 4) + (P[5] << 8)) - (int32_t)(cs << 10);
+        return ((float)lo + (float)hi * 4096.0f) * scale;  // (sum c X - 2^22 sum c) 2^(e-22)
+    }
 };
 
 // Issue point: every load above it issues before the arithmetic below it.
