@@ -271,6 +271,25 @@ def test_config3_mixed_precision_hot_set(gpu, c3, T):
         check_in_block_dispatch(bw, T, got[2], wsd["ws"], tm=bw.workspace_layout(T)["tile_pairs_batched"])
 
 
+def test_config3_batched_wide_range_inputs(gpu, c3):
+    """The batched gate/up's 4-bit limb products (inputs block-scaled per
+    32-element chunk) on inputs whose magnitudes span 2^-40 .. 2^40 inside a
+    chunk, a token of zeros and a token of subnormals: ids and outputs
+    against the oracle at the F32-path tolerance."""
+    blk, bw = c3
+    T = 8
+    rng = np.random.default_rng(77)
+    x = synth.normal(2400, T * 2048).reshape(T, 2048)
+    x = (x * np.exp2(rng.integers(-40, 41, size=x.shape))).astype(np.float32)
+    x[3] = 0.0
+    x[5] = (synth.normal(2401, 2048) * np.float32(1e-39)).astype(np.float32)
+    bias = hot_bias(T, 512, seed=11)
+    got = run_block(gpu, bw, x, T, PATH_AUTO, bias=bias)
+    assert np.all(np.isfinite(got[0]))
+    check_all_ids(blk, got)
+    check_against_oracle(blk, x, got, bias=bias)
+
+
 @pytest.mark.parametrize("experts", [DENSE, (2, 32, BF16), (2, 128, F32), (4, 32, F16),
                                      (8, 64, F16), (8, 128, BF16)])
 @pytest.mark.parametrize("T", [2, 5, 9])
