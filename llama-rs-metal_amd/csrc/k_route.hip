@@ -171,13 +171,17 @@ constexpr int kHistLoads = 8;  // id loads in flight per thread while histogramm
 __global__ __launch_bounds__(kPlaceThreads) void dispatch_kernel(
     const uint32_t *__restrict__ ids, uint32_t pairs, uint32_t E, uint32_t *__restrict__ counts,
     uint32_t *__restrict__ offsets, uint32_t *__restrict__ perm, uint32_t *__restrict__ pos,
-    uint32_t tm, uint32_t *__restrict__ tiles, uint32_t *__restrict__ ntiles) {
+    uint32_t tm, uint32_t *__restrict__ tiles, uint32_t *__restrict__ ntiles, uint32_t per_chunk) {
     extern __shared__ uint32_t sm[];
-    uint32_t *all = sm, *base = sm + E, *cw = sm + 2 * E;  // cw: [kPlaceWaves][E]
+    // cw: [kPlaceWaves][E]; hist (per_chunk): [gridDim.x][E], the counts of
+    // every chunk, so each id costs one LDS atomic (otherwise the pairs
+    // before this chunk are counted a second time into base)
+    uint32_t *all = sm, *base = sm + E, *cw = sm + 2 * E, *hist = cw + kPlaceWaves * E;
     __shared__ uint32_t wsum[kPlaceWaves], tsum[kPlaceWaves];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const uint32_t c0 = blockIdx.x * kPlaceChunk;
-    for (uint32_t i = tid; i < (2 + kPlaceWaves) * E; i += kPlaceThreads) sm[i] = 0u;
+    const uint32_t nsm = (2 + kPlaceWaves) * E + (per_chunk ? gridDim.x * E : 0u);
+    for (uint32_t i = tid; i < nsm; i += kPlaceThreads) sm[i] = 0u;
     __syncthreads();
     // counts of all pairs, and of the pairs before this chunk (kHistLoads
     // loads issued before their atomics)
@@ -191,12 +195,29 @@ __global__ __launch_bounds__(kPlaceThreads) void dispatch_kernel(
 #pragma unroll
         for (int i = 0; i < kHistLoads; i++) {
             if (v[i] < E) {
-                atomicAdd(&all[v[i]], 1u);
-                if (b0 + (uint32_t)(i * kPlaceThreads + tid) < c0) atomicAdd(&base[v[i]], 1u);
+                const uint32_t p = b0 + (uint32_t)(i * kPlaceThreads + tid);
+                if (per_chunk) {
+                    atomicAdd(&hist[(p / kPlaceChunk) * E + v[i]], 1u);
+                } else {
+                    atomicAdd(&all[v[i]], 1u);
+                    if (p < c0) atomicAdd(&base[v[i]], 1u);
+                }
             }
         }
     }
     __syncthreads();
+    if (per_chunk) {
+        for (uint32_t e = tid; e < E; e += kPlaceThreads) {
+            uint32_t acc = 0, before = 0;
+            for (uint32_t c = 0; c < gridDim.x; c++) {
+                if (c == blockIdx.x) before = acc;
+                acc += hist[c * E + e];
+            }
+            all[e] = acc;
+            base[e] = before;
+        }
+        __syncthreads();
+    }
     // exclusive scan over experts: thread t owns experts [t*per, t*per + per)
     const uint32_t per = (E + kPlaceThreads - 1) / kPlaceThreads;
     const uint32_t e0 = min(E, (uint32_t)tid * per), e1 = min(E, e0 + per);
@@ -299,8 +320,11 @@ hipError_t launch_dispatch(Prof *p, hipStream_t s, const uint32_t *ids, uint32_t
     const size_t lds = (size_t)(2 + kPlaceWaves) * experts * sizeof(uint32_t);
     if (lds <= 48 * 1024) {
         const uint32_t nb = pairs ? (pairs + kPlaceChunk - 1) / kPlaceChunk : 1u;
-        return launch_kernel(p, "dispatch", dispatch_kernel, dim3(nb), dim3(kPlaceThreads), lds, s,
-                             ids, pairs, experts, counts, offsets, perm, pos, tm, tiles, ntiles);
+        const size_t lds_chunks = lds + (size_t)nb * experts * sizeof(uint32_t);
+        const uint32_t per_chunk = lds_chunks <= 64 * 1024 ? 1u : 0u;
+        return launch_kernel(p, "dispatch", dispatch_kernel, dim3(nb), dim3(kPlaceThreads),
+                             per_chunk ? lds_chunks : lds, s, ids, pairs, experts, counts, offsets, perm,
+                             pos, tm, tiles, ntiles, per_chunk);
     }
     if (tiles) {
         hipError_t e = launch_dispatch(p, s, ids, pairs, experts, counts, offsets, perm, pos);
