@@ -238,7 +238,10 @@ def test_route_nonfinite(gpu):
 
 
 # ---------------------------------------------------------------- dispatch --
-@pytest.mark.parametrize("T,K,E", [(4096, 8, 128), (64, 10, 512), (1, 10, 512), (777, 3, 40)])
+# (4096, 8, 128) runs the single-pass kernel with per-chunk count tables;
+# (8192, 8, 512) the same kernel without them (16 chunks x 512 experts of
+# tables exceed its 64 KiB of LDS)
+@pytest.mark.parametrize("T,K,E", [(4096, 8, 128), (8192, 8, 512), (64, 10, 512), (1, 10, 512), (777, 3, 40)])
 def test_dispatch_bit_exact(gpu, T, K, E):
     logits = synth.normal(23 + T, T * E).reshape(T, E) + zipf_bias(T, E, 5)
     ids, _ = oracle.route_tokens(logits, K, True)
