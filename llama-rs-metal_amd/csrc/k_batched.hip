@@ -133,6 +133,15 @@ __global__ __launch_bounds__(64) void seg_gateup_kernel(SegArgs a) {
         Lu[q].load(a.w2, rows, ok, cl, lpr);
     }
     loads_issued();
+    // 4-bit codes: the rows' code sums, once per entry (the limb products' offset)
+    uint32_t csg[kSegGateItems][kGateFR], csu[kSegGateItems][kGateFR];
+    if constexpr (BITS == 4) {
+#pragma unroll
+        for (int q = 0; q < kSegGateItems; q++) {
+            Lg[q].template code_sums4<XLimbs>(csg[q]);
+            Lu[q].template code_sums4<XLimbs>(csu[q]);
+        }
+    }
     over_inputs(a.in, in, cl, beg, end, [&](uint32_t p) { return a.perm ? a.perm[p] / a.k : p; },
                 [&](const InChunk &X, uint32_t p) {
                     const float xs = X.sum();
@@ -146,8 +155,8 @@ __global__ __launch_bounds__(64) void seg_gateup_kernel(SegArgs a) {
                         const uint32_t item = blockIdx.x * kSegGateItems + q;
                         float g[kGateFR], u[kGateFR];
                         if constexpr (BITS == 4) {
-                            Lg[q].dot_limbs(xl, xs, g);
-                            Lu[q].dot_limbs(xl, xs, u);
+                            Lg[q].dot_limbs(xl, xs, csg[q], g);
+                            Lu[q].dot_limbs(xl, xs, csu[q], u);
                         } else {
                             Lg[q].dot(X.v, xs, g);
                             Lu[q].dot(X.v, xs, u);

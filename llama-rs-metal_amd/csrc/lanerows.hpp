@@ -106,15 +106,22 @@ struct LaneRows {
             res[f] = ok[f] ? v : 0.f;
         }
     }
-    // The same products for 4-bit rows from the input's limbs (XLimbs).
+    // The same products for 4-bit rows from the input's limbs (XLimbs); cs:
+    // the rows' code sums (code_sums4), fixed over the inputs
     template <typename XL>
-    __device__ __forceinline__ void dot_limbs(const XL &xl, float xsum, float *res) const {
+    __device__ __forceinline__ void dot_limbs(const XL &xl, float xsum, const uint32_t *cs,
+                                              float *res) const {
         static_assert(BITS == 4, "limb products take 4-bit codes");
 #pragma unroll
         for (int f = 0; f < R; f++) {
-            const float v = raw_to_f32<T>(sr[f]) * xl.dot4(c[f].w) + raw_to_f32<T>(br[f]) * xsum;
+            const float v = raw_to_f32<T>(sr[f]) * xl.dot4(c[f].w, cs[f]) + raw_to_f32<T>(br[f]) * xsum;
             res[f] = ok[f] ? v : 0.f;
         }
+    }
+    template <typename XL>
+    __device__ __forceinline__ void code_sums4(uint32_t *cs) const {
+#pragma unroll
+        for (int f = 0; f < R; f++) cs[f] = XL::code_sum4(c[f].w);
     }
 };
 
@@ -166,9 +173,16 @@ struct XLimbs {
             }
         }
     }
+    // sum_j c_j of 32 4-bit codes (the offset term of dot4)
+    static __device__ __forceinline__ uint32_t code_sum4(const uint32_t *w) {
+        uint32_t cs = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) cs = __builtin_amdgcn_udot8(w[i], 0x11111111u, cs, false);
+        return cs;
+    }
     // sum_j c_j x_j for the chunk's 32 4-bit codes (4 words, code j of word i
-    // multiplies element 8i + j)
-    __device__ __forceinline__ float dot4(const uint32_t *w) const {
+    // multiplies element 8i + j); cs = code_sum4(w)
+    __device__ __forceinline__ float dot4(const uint32_t *w, uint32_t cs) const {
         uint32_t P[6];
 #pragma unroll
         for (int l = 0; l < 6; l++) {
@@ -177,9 +191,6 @@ struct XLimbs {
             for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_udot8(w[i], W[l][i], acc, false);
             P[l] = acc;  // <= 32 * 15 * 15
         }
-        uint32_t cs = 0;
-#pragma unroll
-        for (int i = 0; i < 4; i++) cs = __builtin_amdgcn_udot8(w[i], 0x11111111u, cs, false);
         const uint32_t lo = P[0] + (P[1] << 4) + (P[2] << 8);                       // < 2^21
         const int32_t hi = (int32_t)(P[3] + (P[4] << 4) + (P[5] << 8)) - (int32_t)(cs << 10);
         return ((float)lo + (float)hi * 4096.0f) * scale;  // (sum c X - 2^22 sum c) 2^(e-22)
