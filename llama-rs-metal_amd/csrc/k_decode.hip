@@ -228,9 +228,27 @@ constexpr size_t kDownSlotBytes = 48 * 1024;  // beside the 16 KiB combine array
 // so a sub-wave's 16 lanes read consecutive slots); the direct loads fetched
 // the row once per sub-wave (64 / lpr times).  Without a slot (rows too long
 // for the block's LDS), direct loads.
+// With a slot and ff a multiple of 256 the row is fetched first (fetch_row,
+// every lane the same number of 16-byte loads, issued back to back: a caller
+// issues them before its expert-id load) and written to the slot later; the
+// loop of the general form waited for each load before its LDS write.
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+constexpr int kRowLoadsMax = 8;  // ff <= 2048
+struct RowRegs {
+    f32x4v v[kRowLoadsMax];
+};
+__device__ __forceinline__ bool row_in_regs(uint32_t ff) { return ff % 256 == 0 && ff / 256 <= kRowLoadsMax; }
+__device__ __forceinline__ void fetch_row(const float *src, uint32_t ff, int lane, RowRegs &r) {
+    const f32x4v *s4 = reinterpret_cast<const f32x4v *>(src);
+    const uint32_t nper = ff / 256;
+#pragma unroll
+    for (int j = 0; j < kRowLoadsMax; j++)
+        if ((uint32_t)j < nper) r.v[j] = s4[lane + 64 * j];
+}
+
 template <bool SLOTS>
 __device__ __forceinline__ void staged_row(float4 *slot, const float *src, uint32_t ff, int lane,
-                                           uint32_t cl, float *xr) {
+                                           uint32_t cl, float *xr, const RowRegs *pre = nullptr) {
     if constexpr (!SLOTS) {
         XChunk X;
         X.load(src, nullptr, cl);
@@ -239,8 +257,18 @@ __device__ __forceinline__ void staged_row(float4 *slot, const float *src, uint3
         return;
     }
     const uint32_t C = ff / 32, n4 = ff / 4;
-    const float4 *s4 = reinterpret_cast<const float4 *>(src);
-    for (uint32_t w4 = lane; w4 < n4; w4 += 64) slot[(w4 % 8) * C + w4 / 8] = s4[w4];
+    if (pre) {
+        f32x4v *s = reinterpret_cast<f32x4v *>(slot);
+        const uint32_t nper = ff / 256;
+#pragma unroll
+        for (int j = 0; j < kRowLoadsMax; j++) {
+            const uint32_t w4 = lane + 64 * j;
+            if ((uint32_t)j < nper) s[(w4 % 8) * C + w4 / 8] = pre->v[j];
+        }
+    } else {
+        const float4 *s4 = reinterpret_cast<const float4 *>(src);
+        for (uint32_t w4 = lane; w4 < n4; w4 += 64) slot[(w4 % 8) * C + w4 / 8] = s4[w4];
+    }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -268,6 +296,11 @@ __device__ __forceinline__ void down_wave(const DecodeKArgs &a, uint32_t wv, uin
         float part[kDownFR];
         XChunk X;  // this expert's SwiGLU activations (no norm)
         if (kk < a.k) {
+            // the activation row does not depend on the expert id: its loads
+            // go first
+            const bool pre = SLOTS && row_in_regs(a.ff);
+            RowRegs rr;
+            if (pre) fetch_row(a.act + (uint64_t)kk * a.ff, a.ff, (int)(threadIdx.x & 63), rr);
             const uint32_t e = a.ids[kk];
             const float wk = a.weights[kk];
 #pragma unroll
@@ -280,11 +313,15 @@ __device__ __forceinline__ void down_wave(const DecodeKArgs &a, uint32_t wv, uin
             L.load(a.down, rows, ok, cl, C);
             loads_issued();
             MOE_STAMP(kStampDown + blockIdx.x * nw + wv, 1 + q);
-            staged_row<SLOTS>(slot, a.act + (uint64_t)kk * a.ff, a.ff, (int)(threadIdx.x & 63), cl, X.xr);
+            staged_row<SLOTS>(slot, a.act + (uint64_t)kk * a.ff, a.ff, (int)(threadIdx.x & 63), cl, X.xr,
+                              pre ? &rr : nullptr);
             L.dot(X.xr, X.finish(nullptr, 0.f, 0, 0), part);
 #pragma unroll
             for (int f = 0; f < kDownFR; f++) acc_r[f] += part[f] * wk;
         } else {
+            const bool pre = SLOTS && row_in_regs(a.ff);
+            RowRegs rr;
+            if (pre) fetch_row(a.sh_act, a.ff, (int)(threadIdx.x & 63), rr);
 #pragma unroll
             for (int f = 0; f < kDownFR; f++) {
                 const uint32_t r = row0 + f * rpi + sub;
@@ -294,7 +331,7 @@ __device__ __forceinline__ void down_wave(const DecodeKArgs &a, uint32_t wv, uin
             LaneRows<BS, ST, kDownFR> L;
             L.load(a.sd, rows, ok, cl, C);
             loads_issued();
-            staged_row<SLOTS>(slot, a.sh_act, a.ff, (int)(threadIdx.x & 63), cl, X.xr);
+            staged_row<SLOTS>(slot, a.sh_act, a.ff, (int)(threadIdx.x & 63), cl, X.xr, pre ? &rr : nullptr);
             L.dot(X.xr, X.finish(nullptr, 0.f, 0, 0), part);
 #pragma unroll
             for (int f = 0; f < kDownFR; f++) acc_s[f] += part[f];
