@@ -297,12 +297,12 @@ __device__ __forceinline__ void down_wave(const DecodeKArgs &a, uint32_t wv, uin
         XChunk X;  // this expert's SwiGLU activations (no norm)
         if (kk < a.k) {
             // the activation row does not depend on the expert id: its loads
-            // go first
+            // issue behind the id's, before the wait for it
+            const uint32_t e = a.ids[kk];
+            const float wk = a.weights[kk];
             const bool pre = SLOTS && row_in_regs(a.ff);
             RowRegs rr;
             if (pre) fetch_row(a.act + (uint64_t)kk * a.ff, a.ff, (int)(threadIdx.x & 63), rr);
-            const uint32_t e = a.ids[kk];
-            const float wk = a.weights[kk];
 #pragma unroll
             for (int f = 0; f < kDownFR; f++) {
                 const uint32_t r = row0 + f * rpi + sub;
