@@ -80,6 +80,31 @@ def make_layer(gpu, seed):
     return bw, [router, *experts, *shared, sgate]
 
 
+# Captured graphs, one per (issue function, steps per graph): made once, replayed
+# by every later call with the same pair, and destroyed only at the end of
+# main() after the final synchronisation, so no executable is torn down while
+# a profiler may still be recording the dispatches of earlier replays.
+_GRAPHS = {}
+
+
+def graph_of(gpu, issue, n):
+    """The graph of steps issue(b, 0 .. n-1), captured on first use."""
+    g = _GRAPHS.get((issue, n))
+    if g is None:
+        cap = gpu.capture()
+        with cap as b:
+            for j in range(n):
+                issue(b, j)
+        g = _GRAPHS[(issue, n)] = cap.graph
+    return g
+
+
+def release_graphs():
+    for g in _GRAPHS.values():
+        g.destroy()
+    _GRAPHS.clear()
+
+
 def run_graphs(gpu, issue, steps, chunk):
     """`steps` steps as replays of a captured graph of `chunk` steps plus one
     graph of the remainder, in one batch; returns the batch's GPU seconds.
@@ -89,11 +114,7 @@ def run_graphs(gpu, issue, steps, chunk):
         if n == 0 or (n == chunk and steps < chunk):
             graphs.append(None)
             continue
-        cap = gpu.capture()
-        with cap as b:
-            for j in range(n):
-                issue(b, j)
-        graphs.append(cap.graph)
+        graphs.append(graph_of(gpu, issue, n))
     full, rest = graphs
     with gpu.batch() as b:
         for _ in range(steps // chunk):
@@ -154,14 +175,12 @@ def bench_prefill(gpu, bw, iters=10, T=P_T, flops=PREFILL_FLOPS, bias_np=None, w
         for _ in range(iters):
             b.moe_block(bw, x, out, T, ws, logit_bias=bias, ids_out=ids)
     t_eager = b.seconds / iters
-    cap = gpu.capture()
-    with cap as b:
-        b.moe_block(bw, x, out, T, ws, logit_bias=bias, ids_out=ids)
+    graph = graph_of(gpu, lambda b, j: b.moe_block(bw, x, out, T, ws, logit_bias=bias, ids_out=ids), 1)
     with gpu.batch() as b:
-        b.graph(cap.graph)
+        b.graph(graph)
     with gpu.batch() as b:
         for _ in range(iters):
-            b.graph(cap.graph)
+            b.graph(graph)
     t = b.seconds / iters
     counts = np.bincount(gpu.read_u32(ids), minlength=E)
     k_us = {k: round(v[1] / v[0] * 1e6, 2) for k, v in prof.items()}
@@ -613,6 +632,7 @@ def main():
             log(f"[bench] config-5 {v}: {r['us_per_token']} us/token over {STACK_LAYERS} layers, "
                 f"{r['achieved_GBps']} GB/s")
             result["stack"].append(r)
+    release_graphs()  # every batch above has completed (each one ends synchronised)
     print(json.dumps(result), flush=True)
     gpu.close()
 

@@ -51,7 +51,9 @@ struct GemvLaunch {
     uint32_t tokens;
     template <int BITS, int T>
     hipError_t operator()() {
-        if (w.out == 1 && nsel == 1 && w.experts == 1)
+        // (a selected expert id may lie past the single expert: the generic
+        // kernel then writes 0, as affine.metal:91 does)
+        if (w.out == 1 && nsel == 1 && w.experts == 1 && ids == nullptr)
             return launch_kernel(p, "gemv_row1", gemv_row1_kernel<BITS, T>, dim3((tokens + 3) / 4), dim3(256), 0,
                                  s, w, x, y, tokens);
         dim3 grid((w.out + 3) / 4, nsel, tokens);
@@ -65,7 +67,7 @@ hipError_t launch_gemv(Prof *p, hipStream_t s, const WDesc &w, const float *x,
                        uint32_t tokens) {
     if (w.out == 0 || nsel == 0 || tokens == 0) return hipSuccess;
     hipError_t e = hipSuccess;
-    if (nsel == 1 && w.out == 1 && w.experts == 1) {
+    if (nsel == 1 && w.out == 1 && w.experts == 1 && ids == nullptr) {
         e = dispatch_kind(w, GemvLaunch{p, s, w, x, x_sel_stride, ids, 1, y, tokens});
     } else if (nsel == 1) {
         // grid.z is limited to 65535: split long token runs (matmul only).

@@ -135,7 +135,9 @@ struct LaneRows {
 // sum_j c_j X_j = sum_l 16^l udot8(codes, W[l]) exactly; the 2^22 offset is
 // taken off with sum_j c_j.  One rounding of the exact integer sum
 // (2^-23 of the chunk maximum per input, the F32 FMA chain's order of
-// error).  A non-finite input makes the chunk's scale NaN.
+// error).  A non-finite input makes the chunk's scale NaN.  Chunks whose
+// maximum lies below 2^-106 (subnormals included) take e = -105, so 2^(22-e)
+// stays finite and every X_j still fits: their error is 2^-128 per input.
 struct XLimbs {
     uint32_t W[6][4];
     float scale;  // 2^(e - 22)
@@ -143,7 +145,7 @@ struct XLimbs {
         float m = 0.f;
 #pragma unroll
         for (int j = 0; j < 32; j++) m = fmaxf(m, fabsf(x[j]));
-        const int e = __builtin_amdgcn_frexp_expf(m);
+        const int e = max(__builtin_amdgcn_frexp_expf(m), -105);
         const float up = __builtin_amdgcn_ldexpf(1.0f, 22 - e);
         scale = __builtin_isfinite(m) ? __builtin_amdgcn_ldexpf(1.0f, e - 22) : __builtin_nanf("");
 #pragma unroll

@@ -498,14 +498,20 @@ class Gpu:
 
 
 class Graph:
+    """A captured, instantiated graph.  destroy() frees it (call it after the
+    replays have completed); otherwise it is freed on collection."""
+
     def __init__(self, gpu, h):
         self.gpu, self.h = gpu, h
 
+    def destroy(self):
+        if self.h:
+            _lib.moe_graph_destroy(self.h)
+            self.h = None
+
     def __del__(self):
         try:
-            if self.h:
-                _lib.moe_graph_destroy(self.h)
-                self.h = None
+            self.destroy()
         except Exception:
             pass
 

@@ -265,15 +265,25 @@ void orc_add(const float *a, const float *b, float *y, uint64_t n) {
  * dims [in, out]; y[t*out + r] = matvec(decode(W), x[t*in..]).  Same values as
  * the reference test's tensor_core::matvec(&tensor.decode(), x)
  * (crates/metal-backend/tests/affine.rs:70-74). */
+static int em_rows(const float *w, uint64_t rows, uint64_t in, const float *xs, uint64_t ld,
+                   const uint64_t *src, const uint64_t *dst, uint64_t np, float *y,
+                   uint64_t ystride);
+
 int orc_matmul(const orc_weight *w, const float *x, float *y, uint64_t tokens) {
     if (orc_weight_validate(w) || w->ndims != 2 || tokens == 0) return -1;
     uint64_t in = w->dims[0], out = w->dims[1];
     float *dec = (float *)malloc(sizeof(float) * in * out);
-    if (!dec) return -2;
-    orc_weight_decode_rows(w, 0, out, dec);
-    for (uint64_t t = 0; t < tokens; t++) orc_matvec(dec, x + t * in, out, in, y + t * out);
+    uint64_t *idx = (uint64_t *)malloc(sizeof(uint64_t) * tokens);
+    int rc = dec && idx ? 0 : -2;
+    if (rc == 0) {
+        orc_weight_decode_rows(w, 0, out, dec);
+        /* every token's rows are orc_matvec's sums, several tokens at a time */
+        for (uint64_t t = 0; t < tokens; t++) idx[t] = t;
+        rc = em_rows(dec, out, in, x, in, idx, idx, tokens, y, out);
+    }
     free(dec);
-    return 0;
+    free(idx);
+    return rc;
 }
 
 /* Batch::expert_matmul (matrix.rs:149-205) with the kernel semantics of
@@ -414,7 +424,204 @@ done:
     return rc;
 }
 
-/* RMSNorm -> MoE -> residual per layer (execute.rs:197,236). */
+/* ------------------------------------------------- expert-major block -- */
+
+/* Eight input rows advance together through one weight row: lane l of the
+ * vector is input l's running sum.  Each lane is its own sequential
+ * mul-then-add sum from 0 in ascending i -- the sum orc_matvec forms for
+ * that input alone -- so the values are the same bit for bit (vector
+ * arithmetic is element-wise IEEE; -ffp-contract=off forbids fusing). */
+#define EM_LANES 8
+typedef float em_vec __attribute__((vector_size(4 * EM_LANES)));
+
+__attribute__((target_clones("avx2", "default"), noinline)) static void em_kernel(
+    const float *w, uint64_t r0, uint64_t r1, uint64_t in, const em_vec *xt, uint64_t nj,
+    const uint64_t *dst, float *y, uint64_t ystride) {
+    uint64_t r = r0;
+    /* four rows at a time: four independent sums per lane share the loads */
+    for (; r + 4 <= r1; r += 4) {
+        const float *w0 = w + r * in, *w1 = w0 + in, *w2 = w1 + in, *w3 = w2 + in;
+        em_vec a0 = {0}, a1 = {0}, a2 = {0}, a3 = {0};
+        for (uint64_t i = 0; i < in; i++) {
+            const em_vec v = xt[i];
+            a0 += w0[i] * v;
+            a1 += w1[i] * v;
+            a2 += w2[i] * v;
+            a3 += w3[i] * v;
+        }
+        for (uint64_t l = 0; l < nj; l++) {
+            float *yl = y + dst[l] * ystride + r;
+            yl[0] = a0[l];
+            yl[1] = a1[l];
+            yl[2] = a2[l];
+            yl[3] = a3[l];
+        }
+    }
+    for (; r < r1; r++) {
+        const float *wr = w + r * in;
+        em_vec acc = {0};
+        for (uint64_t i = 0; i < in; i++) acc += wr[i] * xt[i];
+        for (uint64_t l = 0; l < nj; l++) y[dst[l] * ystride + r] = acc[l];
+    }
+}
+
+/* y[dst[j]*ystride + r] = sum_i w[r*in+i] * xs[src[j]*ld + i] for rows r of
+ * the decoded weight w (rows x in, row-major) and inputs j < np: one
+ * orc_matvec per input, evaluated eight inputs at a time (same values). */
+static int em_rows(const float *w, uint64_t rows, uint64_t in, const float *xs, uint64_t ld,
+                   const uint64_t *src, const uint64_t *dst, uint64_t np, float *y,
+                   uint64_t ystride) {
+    const uint64_t nb = (np + EM_LANES - 1) / EM_LANES, rc = 32, nr = (rows + rc - 1) / rc;
+    int bad = 0;
+#pragma omp parallel if (rows * in * np >= ORC_PAR_MIN)
+    {
+        em_vec *xt = (em_vec *)aligned_alloc(sizeof(em_vec), sizeof(em_vec) * (in ? in : 1));
+        if (!xt) {
+#pragma omp atomic write
+            bad = 1;
+        }
+#pragma omp for schedule(dynamic, 1)
+        for (uint64_t task = 0; task < nb * nr; task++) {
+            if (!xt) continue;
+            const uint64_t b = task / nr, r0 = (task % nr) * rc;
+            const uint64_t r1 = r0 + rc < rows ? r0 + rc : rows;
+            const uint64_t j0 = b * EM_LANES, nj = np - j0 < EM_LANES ? np - j0 : EM_LANES;
+            for (uint64_t i = 0; i < in; i++)
+                for (uint64_t l = 0; l < EM_LANES; l++)
+                    xt[i][l] = l < nj ? xs[src[j0 + l] * ld + i] : 0.0f;
+            em_kernel(w, r0, r1, in, xt, nj, dst + j0, y, ystride);
+        }
+        free(xt);
+    }
+    return bad ? -2 : 0;
+}
+
+/* orc_moe_block evaluated expert by expert (same outputs bit for bit; test
+ * infrastructure for all-token parity at prefill sizes).  Every token is
+ * routed first (router decoded once, each token's logits the same
+ * sequential sums, plus the bias, then orc_route); the (token, k) pairs of a
+ * chunk of tokens are sorted by expert (orc_dispatch); each expert's
+ * gate/up/down are decoded once per chunk and applied to all its pairs,
+ * each (pair, row) product the sum orc_matvec forms; each token then mixes
+ * its K rows in k order and adds the gated shared expert exactly as
+ * orc_moe_block does (execute.rs:208-233,251-267). */
+int orc_moe_block_em(const orc_moe *m, const float *x, uint32_t tokens, const float *logit_bias,
+                     const float *logits_in, float *out, float *logits_out, uint32_t *ids_out,
+                     float *w_out) {
+    const uint64_t h = m->gate.dims[0], ff = m->gate.dims[1], E = m->gate.dims[2];
+    const uint32_t K = m->k;
+    if (m->router.dims[0] != h || m->router.dims[1] != E || K == 0 || K > E) return -1;
+    if (m->up.dims[0] != h || m->up.dims[1] != ff || m->down.dims[0] != ff ||
+        m->down.dims[1] != h)
+        return -1;
+    if (orc_weight_validate(&m->router) || orc_weight_validate(&m->gate) ||
+        orc_weight_validate(&m->up) || orc_weight_validate(&m->down))
+        return -1;
+    const uint64_t ffs = m->has_shared ? m->sh_gate.dims[1] : 0;
+    const uint32_t CH = 4096;  /* tokens per chunk (bounds the per-pair buffers) */
+    const uint64_t ct = tokens < CH ? tokens : CH;
+    uint64_t wmax = h * E;
+    if (h * ff > wmax) wmax = h * ff;
+    if (h * ffs > wmax) wmax = h * ffs;
+    float *routes = (float *)malloc(sizeof(float) * ((uint64_t)tokens * E + 1));
+    uint32_t *ids = (uint32_t *)malloc(sizeof(uint32_t) * ((uint64_t)tokens * K + 1));
+    float *wts = (float *)malloc(sizeof(float) * ((uint64_t)tokens * K + 1));
+    float *wg = (float *)malloc(sizeof(float) * wmax);
+    float *wu = (float *)malloc(sizeof(float) * wmax);
+    float *wd = (float *)malloc(sizeof(float) * wmax);
+    float *gi = (float *)malloc(sizeof(float) * (h + 1));
+    float *g = (float *)malloc(sizeof(float) * (ct * K * (ff > ffs ? ff : ffs) + 1));
+    float *u = (float *)malloc(sizeof(float) * (ct * K * (ff > ffs ? ff : ffs) + 1));
+    float *eo = (float *)malloc(sizeof(float) * (ct * K * h + 1));
+    float *sg = (float *)malloc(sizeof(float) * (ct + 1));
+    uint64_t *src = (uint64_t *)malloc(sizeof(uint64_t) * (ct * K + tokens + 1));
+    uint64_t *dst = (uint64_t *)malloc(sizeof(uint64_t) * (ct * K + tokens + 1));
+    uint32_t *counts = (uint32_t *)malloc(sizeof(uint32_t) * (E + 1));
+    uint32_t *offsets = (uint32_t *)malloc(sizeof(uint32_t) * (E + 2));
+    uint32_t *perm = (uint32_t *)malloc(sizeof(uint32_t) * (ct * K + 1));
+    int rc = 0;
+    if (!routes || !ids || !wts || !wg || !wu || !wd || !gi || !g || !u || !eo || !sg || !src ||
+        !dst || !counts || !offsets || !perm) {
+        rc = -2;
+        goto done;
+    }
+    /* router (execute.rs:220) and routing (:221) of every token */
+    if (logits_in) {
+        memcpy(routes, logits_in, sizeof(float) * (uint64_t)tokens * E);
+    } else {
+        if (orc_weight_decode_rows(&m->router, 0, E, wg)) { rc = -1; goto done; }
+        for (uint64_t t = 0; t < tokens; t++) src[t] = dst[t] = t;
+        if ((rc = em_rows(wg, E, h, x, h, src, dst, tokens, routes, E))) goto done;
+        if (logit_bias)
+            for (uint64_t i = 0; i < (uint64_t)tokens * E; i++) routes[i] += logit_bias[i];
+    }
+    if (logits_out) memcpy(logits_out, routes, sizeof(float) * (uint64_t)tokens * E);
+    for (uint64_t t = 0; t < tokens; t++)
+        orc_route(routes + t * E, (uint32_t)E, K, (int)m->normalize, ids + t * K, wts + t * K);
+    if (ids_out) memcpy(ids_out, ids, sizeof(uint32_t) * (uint64_t)tokens * K);
+    if (w_out) memcpy(w_out, wts, sizeof(float) * (uint64_t)tokens * K);
+    for (uint64_t t0 = 0; t0 < tokens; t0 += CH) {
+        const uint64_t nt = tokens - t0 < CH ? tokens - t0 : CH;
+        if ((rc = orc_dispatch(ids + t0 * K, (uint32_t)nt, K, (uint32_t)E, counts, offsets, perm,
+                               NULL)))
+            goto done;
+        for (uint64_t e = 0; e < E; e++) {
+            const uint64_t n = counts[e], o = offsets[e];
+            if (!n) continue;
+            /* expert_matmul gate/up (:222-223): pair j of the segment reads its
+             * token's row; swiglu (:224); down on the pair's own row (:225) into
+             * the token's k-th slot of eo */
+            if (orc_weight_decode_rows(&m->gate, e * ff, ff, wg) ||
+                orc_weight_decode_rows(&m->up, e * ff, ff, wu) ||
+                orc_weight_decode_rows(&m->down, e * h, h, wd)) { rc = -1; goto done; }
+            for (uint64_t j = 0; j < n; j++) {
+                src[j] = t0 + perm[o + j] / K;
+                dst[j] = j;
+            }
+            if ((rc = em_rows(wg, ff, h, x, h, src, dst, n, g, ff)) ||
+                (rc = em_rows(wu, ff, h, x, h, src, dst, n, u, ff)))
+                goto done;
+            orc_swiglu(g, u, g, n * ff);
+            for (uint64_t j = 0; j < n; j++) {
+                src[j] = j;
+                dst[j] = perm[o + j];
+            }
+            if ((rc = em_rows(wd, h, ff, g, ff, src, dst, n, eo, h))) goto done;
+        }
+        /* mix (:226) */
+        for (uint64_t t = 0; t < nt; t++)
+            orc_mix(eo + t * K * h, wts + (t0 + t) * K, K, h, out + (t0 + t) * h);
+        if (!m->has_shared) continue;
+        /* shared expert (:228, :251-267), its sigmoid gate (:230-231), add (:232) */
+        if (orc_weight_decode_rows(&m->sh_gate, 0, ffs, wg) ||
+            orc_weight_decode_rows(&m->sh_up, 0, ffs, wu) ||
+            orc_weight_decode_rows(&m->sh_down, 0, h, wd) ||
+            orc_weight_decode_rows(&m->sh_gate_inp, 0, 1, gi)) { rc = -1; goto done; }
+        for (uint64_t t = 0; t < nt; t++) {
+            src[t] = t0 + t;
+            dst[t] = t;
+        }
+        if ((rc = em_rows(wg, ffs, h, x, h, src, dst, nt, g, ffs)) ||
+            (rc = em_rows(wu, ffs, h, x, h, src, dst, nt, u, ffs)) ||
+            (rc = em_rows(gi, 1, h, x, h, src, dst, nt, sg, 1)))
+            goto done;
+        orc_swiglu(g, u, g, nt * ffs);
+        for (uint64_t t = 0; t < nt; t++) src[t] = t;
+        if ((rc = em_rows(wd, h, ffs, g, ffs, src, dst, nt, eo, h))) goto done;
+        for (uint64_t t = 0; t < nt; t++) {
+            float *so = eo + t * h, *proj = out + (t0 + t) * h;
+            orc_gate_scalar(so, sg + t, so, h);
+            orc_add(proj, so, proj, h);
+        }
+    }
+done:
+    free(routes); free(ids); free(wts); free(wg); free(wu); free(wd); free(gi); free(g);
+    free(u); free(eo); free(sg); free(src); free(dst); free(counts); free(offsets); free(perm);
+    return rc;
+}
+
+/* RMSNorm -> MoE -> residual per layer (execute.rs:197,236).  The block is
+ * the expert-major evaluation (the same values as orc_moe_block). */
 int orc_moe_stack(const orc_moe *layers, const float *const *norm_w, uint32_t nlayers,
                   float eps, float *hidden, uint32_t tokens) {
     uint64_t h = layers[0].gate.dims[0];
@@ -424,7 +631,7 @@ int orc_moe_stack(const orc_moe *layers, const float *const *norm_w, uint32_t nl
     for (uint32_t l = 0; l < nlayers && rc == 0; l++) {
         for (uint32_t t = 0; t < tokens; t++)
             orc_rms_norm(hidden + t * h, norm_w[l], h, eps, norm + t * h);
-        rc = orc_moe_block(&layers[l], norm, tokens, NULL, NULL, proj, NULL, NULL, NULL);
+        rc = orc_moe_block_em(&layers[l], norm, tokens, NULL, NULL, proj, NULL, NULL, NULL);
         if (rc == 0) orc_add(hidden, proj, hidden, h * tokens);
     }
     free(norm);

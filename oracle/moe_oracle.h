@@ -23,6 +23,8 @@
  *       numpy stable argsort
  *   orc_moe_block   composition of the above; checked against an independent
  *       float64 numpy restatement on the config-1 fixture
+ *   orc_moe_block_em   equal to orc_moe_block bit for bit (dense, affine,
+ *       shared expert, ties, bias, logits_in, several token chunks)
  *   orc_normal / orc_quantize_affine   this build's own synthetic-input tools
  *       (no reference counterpart); LCG constants follow
  *       crates/llama-rs/tests/common/mod.rs:86-97.
@@ -125,6 +127,15 @@ typedef struct {
 int orc_moe_block(const orc_moe *m, const float *x, uint32_t tokens, const float *logit_bias,
                   const float *logits_in, float *out, float *logits_out, uint32_t *ids_out,
                   float *w_out);
+
+/* orc_moe_block evaluated expert by expert: every token routed first, the
+ * pairs of each chunk of 4096 tokens sorted by expert, each expert decoded
+ * once per chunk for all its pairs.  Same arguments and the same outputs bit
+ * for bit (each product is the same sequential sum); used where the
+ * per-token form is too slow (all tokens at prefill sizes). */
+int orc_moe_block_em(const orc_moe *m, const float *x, uint32_t tokens, const float *logit_bias,
+                     const float *logits_in, float *out, float *logits_out, uint32_t *ids_out,
+                     float *w_out);
 
 /* MoE-only stack step: hidden += moe(rms_norm(hidden, norm_w, eps)) per layer
  * (execute.rs:197,236; tensor-core/src/lib.rs:64-70). */

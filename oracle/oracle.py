@@ -101,6 +101,7 @@ def _declare(L):
         "orc_expert_matmul": (I32, [P, P, P, U32, P, I32]),
         "orc_dispatch": (I32, [P, U32, U32, U32, P, P, P, P]),
         "orc_moe_block": (I32, [P, P, U32, P, P, P, P, P, P]),
+        "orc_moe_block_em": (I32, [P, P, U32, P, P, P, P, P, P]),
         "orc_moe_stack": (I32, [P, P, U32, F32, P, U32]),
         "orc_normal": (None, [U64, U64, F32, F32, P]),
         "orc_quantize_affine": (I32, [P, U64, U32, U32, U32, P, P, P]),
@@ -326,9 +327,11 @@ class MoeSpec:
         return m
 
 
-def moe_block(spec, x, tokens, logit_bias=None, logits_in=None):
+def moe_block(spec, x, tokens, logit_bias=None, logits_in=None, expert_major=False):
     """MoE block composition (crates/model-runtime/src/execute.rs:208-233).
-    Returns (out[T,h], logits[T,E], ids[T,K], weights[T,K])."""
+    Returns (out[T,h], logits[T,E], ids[T,K], weights[T,K]).  With
+    expert_major the same values come from orc_moe_block_em (each expert
+    decoded once per 4096 tokens instead of once per pair)."""
     h = spec.gate.dims[0]
     E = spec.gate.dims[2]
     K = spec.k
@@ -340,8 +343,8 @@ def moe_block(spec, x, tokens, logit_bias=None, logits_in=None):
     lb = None if logit_bias is None else _f32(logit_bias)
     li = None if logits_in is None else _f32(logits_in)
     m = spec.struct()
-    rc = lib().orc_moe_block(C.byref(m), _p(x), tokens, _p(lb), _p(li), _p(out), _p(logits),
-                             _p(ids), _p(w))
+    fn = lib().orc_moe_block_em if expert_major else lib().orc_moe_block
+    rc = fn(C.byref(m), _p(x), tokens, _p(lb), _p(li), _p(out), _p(logits), _p(ids), _p(w))
     if rc:
         raise ValueError("moe block shape")
     return out, logits, ids, w

@@ -125,6 +125,26 @@ def test_expert_matmul_per_expert_input_and_out_of_range_id(gpu):
     assert (gpu.read(out)[10:] == 0).all()
 
 
+def test_expert_matmul_single_row_weight_honours_ids(gpu):
+    """A one-row, one-expert weight ([64, 1, 1]) under expert_matmul with a
+    GPU id: id 0 gives the product, id 5 (>= E) gives 0 (affine.metal:91,
+    matrix.metal:52-55) -- the one-row fast path applies only without ids."""
+    t = _pattern_tensor([64, 1, 1], 4, 32, BF16)
+    w = gpu.weight_tensor(t)
+    x = synth.normal(8, 64)
+    xb = gpu.upload(x)
+    for e in (0, 5):
+        ib, out = gpu.upload_u32(np.array([e], np.uint32)), gpu.zeros(1)
+        with gpu.batch() as b:
+            b.expert_matmul(w, xb, ib, out, False)
+        ref = oracle.expert_matmul(t, x, np.array([e], np.uint32), False)
+        close(gpu.read(out), ref)
+        if e == 5:
+            assert gpu.read(out)[0] == 0.0
+        else:
+            assert ref[0] != 0.0
+
+
 def test_actual_gpu_ops(gpu):
     # crates/metal-backend/tests/operations.rs:8-28
     data = np.sin(np.arange(65 * 7, dtype=np.float32) * np.float32(0.13)).astype(np.float32)
@@ -240,8 +260,11 @@ def test_route_nonfinite(gpu):
 # ---------------------------------------------------------------- dispatch --
 # (4096, 8, 128) runs the single-pass kernel with per-chunk count tables;
 # (8192, 8, 512) the same kernel without them (16 chunks x 512 experts of
-# tables exceed its 64 KiB of LDS)
-@pytest.mark.parametrize("T,K,E", [(4096, 8, 128), (8192, 8, 512), (64, 10, 512), (1, 10, 512), (777, 3, 40)])
+# tables exceed its 64 KiB of LDS); (4096, 10, 512) and (5600, 10, 512) the
+# tables at 10 and 14 chunks over 512 experts (the Qwen3-Next prefill's
+# dispatch), the latter filling the 64 KiB
+@pytest.mark.parametrize("T,K,E", [(4096, 8, 128), (8192, 8, 512), (4096, 10, 512), (5600, 10, 512),
+                                   (64, 10, 512), (1, 10, 512), (777, 3, 40)])
 def test_dispatch_bit_exact(gpu, T, K, E):
     logits = synth.normal(23 + T, T * E).reshape(T, E) + zipf_bias(T, E, 5)
     ids, _ = oracle.route_tokens(logits, K, True)

@@ -391,3 +391,97 @@ def test_threads_do_not_change_results():
         oracle.set_threads(n)
     for a, b in zip(one, many):
         assert np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32))
+
+
+# ------------------------------------------------- expert-major evaluation --
+def _bits(outs):
+    return [np.asarray(a).view(np.uint32) if np.asarray(a).dtype == np.float32 else np.asarray(a)
+            for a in outs]
+
+
+def _same(a, b):
+    for p, q in zip(_bits(a), _bits(b)):
+        assert np.array_equal(p, q)
+
+
+@pytest.mark.parametrize("kind", ["f32", "affine"])
+def test_moe_block_expert_major_equals_per_token_config1(kind):
+    """orc_moe_block_em (every expert decoded once for all its pairs) gives
+    orc_moe_block's outputs, logits, ids and weights bit for bit on the
+    config-1 fixture: each (pair, row) product is the same sequential sum."""
+    blk, x = config1(kind)
+    _same(oracle.moe_block(blk.spec(), x, 4), oracle.moe_block(blk.spec(), x, 4, expert_major=True))
+
+
+@pytest.mark.parametrize("normalize", [True, False])
+def test_moe_block_expert_major_chunks_shared_bias(normalize):
+    """Mixed weight kinds (8-bit router and shared gate row, f16-scaled 4-bit
+    experts, F32-scaled 2-bit shared expert), a logit bias and 4100 tokens,
+    so the pairs are sorted in two chunks (4096 + 4): bit for bit equal."""
+    kinds = {"router": (8, 64, BF16), "experts": (4, 32, F16), "shared": (2, 32, F32),
+             "shared_gate": (8, 64, BF16)}
+    blk = HostBlock(64, 8, 3, 32, 96, kinds, seed=5, normalize=normalize, random_experts=True)
+    T = 4100
+    x = synth.normal(7, T * 64).reshape(T, 64)
+    rng = np.random.default_rng(3)
+    bias = (rng.standard_normal((T, 8)) * 2).astype(np.float32)
+    a = oracle.moe_block(blk.spec(), x, T, logit_bias=bias)
+    b = oracle.moe_block(blk.spec(), x, T, logit_bias=bias, expert_major=True)
+    _same(a, b)
+    assert len(np.unique(a[2][:, 0])) == 8  # every expert receives pairs
+
+
+def test_moe_block_expert_major_ties_and_logits_in():
+    """Routing of given logits with heavy ties (ids to the lower index) and
+    K = E, so every expert holds every token: expert-major equals per-token."""
+    kinds = {"router": DENSE, "experts": (8, 32, BF16)}
+    blk = HostBlock(96, 6, 6, 32, 0, kinds, seed=9, random_experts=True)
+    T = 37
+    x = synth.normal(11, T * 96).reshape(T, 96)
+    lg = np.round(synth.normal(12, T * 6).reshape(T, 6)).astype(np.float32)  # integers: ties
+    a = oracle.moe_block(blk.spec(), x, T, logits_in=lg)
+    b = oracle.moe_block(blk.spec(), x, T, logits_in=lg, expert_major=True)
+    _same(a, b)
+    for t in range(T):
+        assert a[2][t].tolist() == _expected_ids(lg[t].tolist(), 6)
+
+
+def test_moe_block_expert_major_prefill_shape():
+    """Config-4 shapes (h 2048, E 128, top 8, ff 768, 4-bit g64) at 48 tokens
+    under the Zipf skew: expert-major equals per-token bit for bit."""
+    from helpers import config4, zipf_bias
+    blk = config4()
+    T = 48
+    x = synth.normal(4000, T * 2048).reshape(T, 2048)
+    bias = zipf_bias(T, 128, seed=4)
+    _same(oracle.moe_block(blk.spec(), x, T, logit_bias=bias),
+          oracle.moe_block(blk.spec(), x, T, logit_bias=bias, expert_major=True))
+
+
+def test_matmul_tokens_equal_per_token_matvec():
+    """orc_matmul over many tokens (decoded once, eight tokens per pass) gives
+    each token's orc_matvec of the decoded rows bit for bit."""
+    from helpers import make_tensor
+    t = make_tensor([320, 40], (4, 64, BF16), seed=21)
+    T = 13
+    x = synth.normal(22, T * 320).reshape(T, 320)
+    got = oracle.matmul(t, x, T).reshape(T, 40)
+    dec = oracle.decode(t)
+    for i in range(T):
+        assert np.array_equal(got[i].view(np.uint32), oracle.matvec(dec, x[i]).view(np.uint32))
+
+
+def test_moe_stack_equals_chained_per_token_blocks():
+    """orc_moe_stack (expert-major blocks) over 3 layers with distinct norm
+    weights equals RMSNorm -> orc_moe_block -> add chained by hand."""
+    kinds = {"router": DENSE, "experts": (2, 32, BF16), "shared": (2, 32, BF16), "shared_gate": DENSE}
+    blk = HostBlock(128, 16, 4, 64, 64, kinds, seed=13, random_experts=True)
+    nws = [(1.0 + 0.3 * synth.normal(50 + l, 128)).astype(np.float32) for l in range(3)]
+    x = synth.normal(60, 2 * 128).reshape(2, 128)
+    got = oracle.moe_stack([blk.spec()] * 3, nws, 1e-6, x, 2)
+    h = x.copy()
+    for nw in nws:
+        xn = np.stack([oracle.rms_norm(r, nw, 1e-6) for r in h])
+        out, *_ = oracle.moe_block(blk.spec(), xn, 2)
+        h = oracle.add(h, out).reshape(h.shape)
+    assert np.array_equal(got.view(np.uint32), h.view(np.uint32))
