@@ -215,19 +215,21 @@ QN_FLOPS = 2 * QN_T * K * 3 * H * FF + 2 * QN_T * 3 * H * FFS  # routed + shared
 def bench_prefill_qwen3next(gpu, layer):
     """A Qwen3-Next-shaped prefill (config-2 shapes: E 512, top 10, ff 512,
     shared ff 512, F32 router, 4-bit g64 experts and shared expert) of 4096
-    tokens over layer 0 of the decode leg, with the experts' MFMA tile-order
-    copies: the shared expert runs as one all-token segment of the grouped
-    bf16 GEMM, on the side stream."""
+    tokens over layer 0 of the decode leg, with the MFMA tile-order copies of
+    the routed and the shared experts: the shared expert runs as one more
+    segment of the routed experts' bf16 GEMMs, its gate input from the
+    router's pass over x."""
     bw0, ws0 = layer
     router, g, u, d = ws0[:4]
     pk = [gpu.pack_weight(t) for t in (g, u, d)]
     _, _, _, _, shared, sgate = bw0.keep
-    bw = BlockWeights(router, g, u, d, K, True, shared, sgate, packed=pk)
+    spk = [gpu.pack_weight(t) for t in shared]
+    bw = BlockWeights(router, g, u, d, K, True, shared, sgate, packed=pk, shared_packed=spk)
     r = bench_prefill(gpu, bw, T=QN_T, flops=QN_FLOPS, bias_np=np.zeros((QN_T, E), np.float32),
                       workload="Qwen3-Next-shaped MoE layer prefill, 4096 tokens (config-2 shapes: h2048 "
                                "E512 top10 ff512 + shared ff512, 4-bit g64 bf16 quantized from N(0,0.02), "
-                               "F32 router, no skew), shared expert on the grouped bf16 GEMM")
-    for p_ in pk:
+                               "F32 router, no skew), shared expert as one more segment of the bf16 GEMMs")
+    for p_ in pk + spk:
         for b_ in p_.buffers:
             gpu.release(b_)
     return r
@@ -502,6 +504,7 @@ def main():
     gpu = Gpu(0)
     if args.traffic_probe:
         traffic_probe(gpu, args.traffic_probe)
+        release_graphs()
         gpu.close()
         return
     log(f"[bench] device {gpu.name}; generating {LAYERS} config-2 layers on the GPU")

@@ -217,6 +217,12 @@ typedef struct {
     moe_packed_weight gate_packed;
     moe_packed_weight up_packed;
     moe_packed_weight down_packed;
+    /* the same for the shared expert's gate/up/down: the bf16 MFMA path runs
+     * the shared expert as one more segment of the routed experts' GEMMs when
+     * its weights are of the routed experts' kind and width */
+    moe_packed_weight shared_gate_packed;
+    moe_packed_weight shared_up_packed;
+    moe_packed_weight shared_down_packed;
 } moe_block_weights;
 
 /* Byte sizes of the packed copy of w (the codes; the scales and the biases

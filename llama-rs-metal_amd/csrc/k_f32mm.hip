@@ -27,7 +27,12 @@
 // loads and not stored.  With `xb16`, the blocks of the first expert column
 // also store x rounded to bf16 (to nearest even) for the bf16 expert GEMMs,
 // from the same staging registers: every (token, K range) is staged by
-// exactly one of them, so x is read once for both products.
+// exactly one of them, so x is read once for both products.  With `grow`
+// (a dense F32 row: the shared expert's gate input, [h] reshaped [h, 1],
+// crates/model-runtime/src/loader.rs:194), the same blocks also form x . grow
+// from those registers, one partial sum per token, K range and expert column
+// (each column takes every `columns`-th iteration) in gout[kr][column][t]
+// (execute.rs:230 without a second pass over x).
 #include <type_traits>
 
 #include "rowdot.hpp"
@@ -47,6 +52,7 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kIter = 64;                // K values per iteration (32 per lane half)
 constexpr int kRow = kIter + 4;          // LDS floats per token row (16-byte pad: no bank conflicts)
 constexpr uint32_t kTargetWaves = 2048;  // 2 per SIMD on 256 CUs
+constexpr uint32_t kGateMax = 4096;      // K values of a range whose gate row is staged in LDS
 
 // One lane's 32 weight values of one iteration, raw (as loaded).
 template <int BITS, int T>
@@ -109,13 +115,16 @@ __device__ __forceinline__ void decode_w(const WRaw<BITS, T> &o, int j, float *v
     }
 }
 
-template <int BITS, int T>
+template <int BITS, int T, bool GATE>
 __global__ __launch_bounds__(kThreads) void f32mm_kernel(WDesc r, const float *__restrict__ x,
                                                               uint32_t tokens, uint32_t ksplit,
                                                               const float *__restrict__ bias,
                                                               float *__restrict__ out,
-                                                              uint16_t *__restrict__ xb16) {
+                                                              uint16_t *__restrict__ xb16,
+                                                              const float *__restrict__ grow,
+                                                              float *__restrict__ gout) {
     __shared__ __attribute__((aligned(16))) float xs[2][32 * kRow];
+    __shared__ __attribute__((aligned(16))) float gs[GATE ? kGateMax : 4];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const uint32_t i = lane & 31, hf = lane >> 5;
     const uint32_t h = r.in, E = r.out;
@@ -132,6 +141,16 @@ __global__ __launch_bounds__(kThreads) void f32mm_kernel(WDesc r, const float *_
     f32x16 acc = {};
     f32x4 xr[2][2];  // native vectors: HIP's float4 struct would stay in scratch
     WRaw<BITS, T> wr[2];
+    // shared-gate row (GATE): the block's K range of it goes to LDS once
+    // (klen <= kGateMax, checked on the host); every thread multiplies the x
+    // values it stages with the matching gate values (no loads in the loop,
+    // no branch); the first expert column stores the sums
+    float gsum = 0.f;
+    if constexpr (GATE) {
+        for (uint32_t k = 4 * tid; k < klen; k += 4 * kThreads)
+            *reinterpret_cast<f32x4 *>(&gs[k]) = *reinterpret_cast<const f32x4 *>(grow + kbeg + k);
+        __syncthreads();  // before the first staging reads it
+    }
     auto gload_x = [&](int q, uint32_t it) __attribute__((always_inline)) {
         xr[q][0] = xg[it * (kIter / 4)];
         xr[q][1] = xg[it * (kIter / 4) + 8];
@@ -146,6 +165,19 @@ __global__ __launch_bounds__(kThreads) void f32mm_kernel(WDesc r, const float *_
         if (copy && it < iters) {
             *reinterpret_cast<bf16x4 *>(xbrow + it * kIter) = __builtin_convertvector(xr[q][0], bf16x4);
             *reinterpret_cast<bf16x4 *>(xbrow + it * kIter + 32) = __builtin_convertvector(xr[q][1], bf16x4);
+        }
+        if constexpr (GATE) {
+            // expert column y takes the iterations it % columns == y (uniform:
+            // the columns share the work, so no block's span grows by all of it)
+            if (it < iters && it % gridDim.y == blockIdx.y) {
+                const uint32_t k0 = it * kIter + 4 * sch;
+                const f32x4 g0 = *reinterpret_cast<const f32x4 *>(&gs[k0]);
+                const f32x4 g1 = *reinterpret_cast<const f32x4 *>(&gs[k0 + 32]);
+#pragma unroll
+                for (int c = 0; c < 4; c++) gsum += xr[q][0][c] * g0[c];
+#pragma unroll
+                for (int c = 0; c < 4; c++) gsum += xr[q][1][c] * g1[c];
+            }
         }
     };
     // one iteration: MFMA s of half j multiplies x[i][32hf + 16j + s] with
@@ -194,6 +226,13 @@ __global__ __launch_bounds__(kThreads) void f32mm_kernel(WDesc r, const float *_
         iteration(it, std::integral_constant<int, 0>{});
         iteration(it + 1, std::integral_constant<int, 1>{});
     }
+    if constexpr (GATE) {
+        // the 8 threads of a token row hold its partial sums
+        gsum += __shfl_xor(gsum, 1, 64);
+        gsum += __shfl_xor(gsum, 2, 64);
+        gsum += __shfl_xor(gsum, 4, 64);
+        if (sch == 0 && t0 + srow < tokens) gout[((uint64_t)kr * gridDim.y + blockIdx.y) * tokens + t0 + srow] = gsum;
+    }
     // acc[q] = C[8(q/4) + 4(lane/32) + (q%4)][lane%32]: token row, expert column
     const uint32_t e = e0 + i;
     if (e >= E) return;
@@ -219,15 +258,23 @@ struct Launch {
     const float *bias;
     float *out;
     uint16_t *xb16;
+    const float *grow;
+    float *gout;
     template <int BITS, int T>
     hipError_t operator()() {
         const dim3 grid((tokens + 31) / 32, (r.out + 32 * kWaves - 1) / (32 * kWaves), ksplit);
-        return launch_kernel(p, name, f32mm_kernel<BITS, T>, grid, dim3(kThreads), 0, s, r, x, tokens, ksplit,
-                             bias, out, xb16);
+        if (grow)
+            return launch_kernel(p, name, f32mm_kernel<BITS, T, true>, grid, dim3(kThreads), 0, s, r, x, tokens,
+                                 ksplit, bias, out, xb16, grow, gout);
+        return launch_kernel(p, name, f32mm_kernel<BITS, T, false>, grid, dim3(kThreads), 0, s, r, x, tokens,
+                             ksplit, bias, out, xb16, grow, gout);
     }
 };
 
 }  // namespace f32mm
+
+uint32_t f32mm_gate_max() { return f32mm::kGateMax; }
+uint32_t f32mm_columns(const WDesc &w) { return (w.out + 32 * f32mm::kWaves - 1) / (32 * f32mm::kWaves); }
 
 bool f32mm_supported(const WDesc &r, const float *x) {
     const bool kind = r.bits == 0 ? (r.type == 0 || r.type == 1 || r.type == 30)
@@ -251,9 +298,12 @@ uint32_t f32mm_ksplit(const WDesc &r, uint32_t tokens, uint64_t part_floats) {
 }
 
 hipError_t launch_f32mm(Prof *p, hipStream_t s, const char *name, const WDesc &r, const float *x,
-                        uint32_t tokens, uint32_t ksplit, const float *bias, float *out, uint16_t *xb16) {
+                        uint32_t tokens, uint32_t ksplit, const float *bias, float *out, uint16_t *xb16,
+                        const float *grow, float *gout) {
     if (tokens == 0 || ksplit == 0 || r.in % (ksplit * 2 * f32mm::kIter)) return hipErrorInvalidValue;
-    return dispatch_kind(r, f32mm::Launch{p, s, name, r, x, tokens, ksplit, bias, out, xb16});
+    if (grow && (!gout || (reinterpret_cast<uintptr_t>(grow) & 15u) || r.in / ksplit > f32mm::kGateMax))
+        return hipErrorInvalidValue;
+    return dispatch_kind(r, f32mm::Launch{p, s, name, r, x, tokens, ksplit, bias, out, xb16, grow, gout});
 }
 
 }  // namespace moehip

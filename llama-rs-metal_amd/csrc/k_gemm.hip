@@ -127,6 +127,11 @@ struct Args {
     uint32_t k;                // experts per token
     uint32_t n_tiles_n;        // N-tiles per M-tile
     PackedW pk, pk2;           // affine GATEUP/DOWN: MFMA tile-order copies of w, w2 (or nulls)
+    uint32_t a_base;           // perm null: pair p reads row p - a_base of a_rows
+    // one more segment after the routed ones (the shared expert; affine_gemm_kernel
+    // only): sh_mt M-tiles over positions [sh_base, sh_base + sh_rows), whose
+    // weights and A rows the kernel's second Args describes
+    uint32_t sh_mt, sh_base, sh_rows;
 };
 
 // Per-thread source of kBVals consecutive K values of one weight row: the code
@@ -462,7 +467,7 @@ __device__ __forceinline__ void affine_item(const Args &a, uint8_t *abuf, uint32
         const uint32_t r = 8 * kAfWaves * i + drow;
         uint32_t pos = m0 + r;
         if (pos >= seg_end) pos = m0;
-        const uint32_t src = MODE == GATEUP && a.perm ? a.perm[pos] / a.k : pos;
+        const uint32_t src = MODE == GATEUP && a.perm ? a.perm[pos] / a.k : pos - a.a_base;
         aoff[i] = src * in * 2 + (a_chunk(r, dpos) << 4);
     }
     // B: weight row n of tile t; rows past `out` read row 0 (never stored)
@@ -777,32 +782,56 @@ __device__ __forceinline__ void affine_live(const Args &a, uint8_t *abuf, uint32
 // Affine GATEUP / DOWN products: same persistent XCD-range schedule as
 // grouped_gemm_kernel, kAfWaves waves per block, at most 256 VGPRs per lane so
 // two waves share a SIMD.
+// M-tile position p of the item order when sh shared-expert M-tiles are
+// spread evenly over r + sh positions (shared tile j at position
+// floor((2j + 1)(r + sh) / (2 sh)), so every XCD range holds its share;
+// the routed tiles keep their order): returns the shared tile's index and
+// sets `shared`, or the routed tile's index.
+__device__ __forceinline__ uint32_t tile_at(uint32_t p, uint32_t r, uint32_t sh, bool &shared) {
+    shared = false;
+    if (sh == 0) return p;
+    const uint64_t m = (uint64_t)r + sh;
+    const int64_t num = 2 * (int64_t)sh * (p + 1) - (int64_t)m;  // shared positions <= p: ceil(num / 2m)
+    const uint32_t c = num <= 0 ? 0u : (uint32_t)min((uint64_t)sh, ((uint64_t)num + 2 * m - 1) / (2 * m));
+    if (c > 0 && (uint64_t)(2 * c - 1) * m / (2 * sh) == p) {
+        shared = true;
+        return c - 1;
+    }
+    return p - c;
+}
+
 template <int MODE, int BITS, int T>
 __global__ __attribute__((amdgpu_flat_work_group_size(kAfThreads, kAfThreads), amdgpu_waves_per_eu(2, 2)))
-void affine_gemm_kernel(Args a) {
+void affine_gemm_kernel(Args a, Args ash) {
     static_assert(MODE == GATEUP || MODE == DOWN, "affine_gemm_kernel: expert products only");
     static_assert(BITS == 2 || BITS == 4 || BITS == 8, "affine_gemm_kernel: affine weights only");
     __shared__ __attribute__((aligned(16))) uint8_t abuf[2 * kAfATile + kAfWaves * kEpiBytes];
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t items = *a.ntiles * a.n_tiles_n;
+    const uint32_t routed = *a.ntiles;
+    const uint32_t items = (routed + a.sh_mt) * a.n_tiles_n;
     const uint32_t xcd = blockIdx.x % kXcds, q = blockIdx.x / kXcds, nq = gridDim.x / kXcds;
     const uint32_t per_xcd = (items + kXcds - 1) / kXcds;
     const uint32_t lo = xcd * per_xcd, hi = min(items, lo + per_xcd);
     for (uint32_t item = lo + q; item < hi; item += nq) {
-        const uint32_t mt = item / a.n_tiles_n, nt = item % a.n_tiles_n;
-        const uint32_t e = a.tiles[2 * mt], m0 = a.tiles[2 * mt + 1];
-        const uint32_t seg_end = a.offsets[e + 1];
+        const uint32_t nt = item % a.n_tiles_n;
+        bool sh;
+        const uint32_t mt = tile_at(item / a.n_tiles_n, routed, a.sh_mt, sh);
+        // the shared expert's tiles: expert 0 of its own weights
+        const Args &aa = sh ? ash : a;
+        const uint32_t e = sh ? 0u : a.tiles[2 * mt];
+        const uint32_t m0 = sh ? a.sh_base + kTM * mt : a.tiles[2 * mt + 1];
+        const uint32_t seg_end = sh ? a.sh_base + a.sh_rows : a.offsets[e + 1];
         const uint32_t live = min(seg_end - m0, (uint32_t)kTM);
         if constexpr (T == 0) {
-            affine_live<MODE, BITS, T, 0, false>(a, abuf, nt, e, m0, seg_end, live, lane, wv);
-        } else if (a.pk.data) {
-            if (a.w.gshift == 5) affine_live<MODE, BITS, T, 5, true>(a, abuf, nt, e, m0, seg_end, live, lane, wv);
-            else if (a.w.gshift == 6) affine_live<MODE, BITS, T, 6, true>(a, abuf, nt, e, m0, seg_end, live, lane, wv);
-            else affine_live<MODE, BITS, T, 7, true>(a, abuf, nt, e, m0, seg_end, live, lane, wv);
+            affine_live<MODE, BITS, T, 0, false>(aa, abuf, nt, e, m0, seg_end, live, lane, wv);
+        } else if (aa.pk.data) {
+            if (aa.w.gshift == 5) affine_live<MODE, BITS, T, 5, true>(aa, abuf, nt, e, m0, seg_end, live, lane, wv);
+            else if (aa.w.gshift == 6) affine_live<MODE, BITS, T, 6, true>(aa, abuf, nt, e, m0, seg_end, live, lane, wv);
+            else affine_live<MODE, BITS, T, 7, true>(aa, abuf, nt, e, m0, seg_end, live, lane, wv);
         } else {
-            if (a.w.gshift == 5) affine_live<MODE, BITS, T, 5, false>(a, abuf, nt, e, m0, seg_end, live, lane, wv);
-            else if (a.w.gshift == 6) affine_live<MODE, BITS, T, 6, false>(a, abuf, nt, e, m0, seg_end, live, lane, wv);
-            else affine_live<MODE, BITS, T, 7, false>(a, abuf, nt, e, m0, seg_end, live, lane, wv);
+            if (aa.w.gshift == 5) affine_live<MODE, BITS, T, 5, false>(aa, abuf, nt, e, m0, seg_end, live, lane, wv);
+            else if (aa.w.gshift == 6) affine_live<MODE, BITS, T, 6, false>(aa, abuf, nt, e, m0, seg_end, live, lane, wv);
+            else affine_live<MODE, BITS, T, 7, false>(aa, abuf, nt, e, m0, seg_end, live, lane, wv);
         }
     }
 }
@@ -811,7 +840,7 @@ template <int MODE>
 struct Launch {
     Prof *p;
     hipStream_t s;
-    const Args &a;
+    const Args &a, &ash;
     uint32_t blocks;
     bool affine;  // affine_gemm_kernel (affine_blocks blocks)
     uint32_t affine_blocks;
@@ -821,7 +850,7 @@ struct Launch {
         if constexpr (BITS != 0) {
             if (affine)
                 return launch_kernel(p, name, affine_gemm_kernel<MODE, BITS, T>, dim3(affine_blocks),
-                                     dim3(kAfThreads), 0, s, a);
+                                     dim3(kAfThreads), 0, s, a, ash);
         }
         return launch_kernel(p, name, grouped_gemm_kernel<MODE, BITS, T>, dim3(blocks), dim3(kThreads),
                              kLdsBytes, s, a);
@@ -865,11 +894,24 @@ struct SetLds {
     }
 };
 
+static bool same_kind(const WDesc &a, const WDesc &b) {
+    return a.bits == b.bits && a.type == b.type && a.gshift == b.gshift;
+}
+
+bool gemm_shared_fold_ok(const WDesc &g, const WDesc &u, const WDesc &d, const WDesc &sg, const WDesc &su,
+                         const WDesc &sd, uint64_t T, uint64_t K) {
+    const uint64_t pairs = T * K + T;  // act16 rows: the routed pairs, then the shared rows
+    return g.bits != 0 && same_kind(g, u) && same_kind(g, sg) && same_kind(g, su) && same_kind(d, sd) &&
+           sg.out == g.out && su.out == g.out && sg.in == g.in && sd.in == d.in && sd.out == d.out &&
+           affine_fits(g, T) && affine_fits(u, T) && affine_fits(sg, T) && affine_fits(su, T) &&
+           affine_fits(d, pairs) && affine_fits(sd, pairs) && pairs < (1ull << 31);
+}
+
 hipError_t launch_grouped_gemm(Prof *p, hipStream_t s, int down, const WDesc &w, const WDesc &w2,
                                const PackedW &pk, const PackedW &pk2, const uint16_t *a_rows,
                                uint64_t a_rows_n, const uint32_t *perm, const uint32_t *offsets,
                                const uint32_t *tiles, const uint32_t *ntiles, uint32_t k,
-                               uint16_t *out, const char *name) {
+                               uint16_t *out, const char *name, const SharedSeg *sh) {
     if (!name) name = down ? "gemm_down" : "gemm_gateup";
     gemm::Args a{};
     a.w = w;
@@ -890,15 +932,35 @@ hipError_t launch_grouped_gemm(Prof *p, hipStream_t s, int down, const WDesc &w,
         a.pk = pk;
         a.pk2 = pk2;
     }
+    // the shared expert: same kernel, its own weights; the gate/up product
+    // reads the token's row (position - base), the down product its own rows
+    gemm::Args ash = a;
+    if (sh) {
+        if (!affine || !same_kind(sh->w, w) || !same_kind(sh->w2, w) || sh->w.out != w.out ||
+            sh->w.in != w.in || !affine_fits(sh->w, a_rows_n) || !affine_fits(sh->w2, a_rows_n))
+            return hipErrorInvalidValue;
+        ash.w = sh->w;
+        ash.w2 = sh->w2;
+        ash.pk = ash.pk2 = PackedW{};
+        if (w.type != 0 && sh->pk.data && sh->pk2.data) {
+            ash.pk = sh->pk;
+            ash.pk2 = sh->pk2;
+        }
+        ash.perm = nullptr;
+        ash.a_base = down ? 0u : sh->base;
+        a.sh_mt = ash.sh_mt = (sh->rows + gemm::kTM - 1) / gemm::kTM;
+        a.sh_base = ash.sh_base = sh->base;
+        a.sh_rows = ash.sh_rows = sh->rows;
+    }
     hipError_t e;
     if (down) {
         a.n_tiles_n = affine ? (w.out + 64 * gemm::kAfWaves - 1) / (64 * gemm::kAfWaves) : (w.out + gemm::kTN - 1) / gemm::kTN;
         if (!affine && (e = dispatch_kind(w, SetLds<gemm::DOWN>{})) != hipSuccess) return e;
-        e = dispatch_kind(w, gemm::Launch<gemm::DOWN>{p, s, a, blocks, affine, affine_blocks, name});
+        e = dispatch_kind(w, gemm::Launch<gemm::DOWN>{p, s, a, ash, blocks, affine, affine_blocks, name});
     } else {
         a.n_tiles_n = affine ? (w.out + 32 * gemm::kAfWaves - 1) / (32 * gemm::kAfWaves) : (w.out + gemm::kTN / 2 - 1) / (gemm::kTN / 2);
         if (!affine && (e = dispatch_kind(w, SetLds<gemm::GATEUP>{})) != hipSuccess) return e;
-        e = dispatch_kind(w, gemm::Launch<gemm::GATEUP>{p, s, a, blocks, affine, affine_blocks, name});
+        e = dispatch_kind(w, gemm::Launch<gemm::GATEUP>{p, s, a, ash, blocks, affine, affine_blocks, name});
     }
     return e;
 }

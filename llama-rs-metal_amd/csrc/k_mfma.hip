@@ -141,6 +141,14 @@ __global__ __launch_bounds__(256) void identity_schedule_kernel(uint32_t T, uint
     }
 }
 
+// The shared expert's gate input of token t: the sum of ks partial sums over
+// K ranges, in range order.
+__device__ __forceinline__ float gate_input(const float *g, uint32_t ks, uint32_t tokens, uint32_t t) {
+    float v = g[t];
+    for (uint32_t r = 1; r < ks; r++) v += g[(uint64_t)r * tokens + t];
+    return v;
+}
+
 // The shared expert's output element o: F32 (sh_out) or bf16 (sh16).
 __device__ __forceinline__ float shared_value(const float *sh_out, const uint16_t *sh16, uint64_t o) {
     return sh16 ? __uint_as_float((uint32_t)sh16[o] << 16) : sh_out[o];
@@ -154,7 +162,7 @@ __global__ __launch_bounds__(256) void combine16_kernel(const uint16_t *__restri
                                                         const uint16_t *__restrict__ sh16,
                                                         const float *__restrict__ sh_gate,
                                                         const float *__restrict__ resid,
-                                                        float *__restrict__ out, uint32_t h) {
+                                                        float *__restrict__ out, uint32_t h, uint32_t gks) {
     const uint32_t t = blockIdx.y;
     for (uint32_t i = 2 * (blockIdx.x * 256 + threadIdx.x); i < h; i += 2 * 256 * gridDim.x) {
         float v0 = 0.f, v1 = 0.f;
@@ -167,7 +175,7 @@ __global__ __launch_bounds__(256) void combine16_kernel(const uint16_t *__restri
         }
         const uint64_t o = (uint64_t)t * h + i;
         if (sh_out || sh16) {
-            const float d = 1.0f + expf(-sh_gate[t]);
+            const float d = 1.0f + expf(-gate_input(sh_gate, gks, gridDim.y, t));
             v0 = v0 + shared_value(sh_out, sh16, o) / d;
             v1 = v1 + shared_value(sh_out, sh16, o + 1) / d;
         }
@@ -204,12 +212,14 @@ hipError_t launch_mfma_experts(Prof *p, hipStream_t s, const WDesc &gate, const 
                                const WDesc &down, const PackedW &pg, const PackedW &pu,
                                const PackedW &pd, const uint16_t *xb16, uint32_t tokens,
                                const uint32_t *offsets, const uint32_t *perm, uint32_t k,
-                               uint32_t *tiles, uint32_t *ntiles, uint16_t *act16, uint16_t *y16) {
+                               uint32_t *tiles, uint32_t *ntiles, uint16_t *act16, uint16_t *y16,
+                               const SharedSeg *sh_gu, const SharedSeg *sh_dn) {
     hipError_t e = launch_grouped_gemm(p, s, 0, gate, up, pg, pu, xb16, tokens, perm, offsets, tiles, ntiles, k,
-                            act16);
+                                       act16, nullptr, sh_gu);
     if (e != hipSuccess) return e;
-    return launch_grouped_gemm(p, s, 1, down, down, pd, pd, act16, (uint64_t)tokens * k, perm, offsets,
-                               tiles, ntiles, k, y16);
+    const uint64_t rows = (uint64_t)tokens * k + (sh_dn ? tokens : 0u);
+    return launch_grouped_gemm(p, s, 1, down, down, pd, pd, act16, rows, perm, offsets, tiles, ntiles, k, y16,
+                               nullptr, sh_dn);
 }
 
 // Same combine with 8 columns per thread (16-byte row loads, all K rows of a
@@ -223,7 +233,7 @@ __global__ __launch_bounds__(256) void combine16v_kernel(const uint16_t *__restr
                                                          const uint16_t *__restrict__ sh16,
                                                          const float *__restrict__ sh_gate,
                                                          const float *__restrict__ resid,
-                                                         float *__restrict__ out, uint32_t h) {
+                                                         float *__restrict__ out, uint32_t h, uint32_t gks) {
     const uint32_t t = blockIdx.y;
     const uint32_t i = 8 * (blockIdx.x * blockDim.x + threadIdx.x);
     if (i >= h) return;
@@ -256,7 +266,7 @@ __global__ __launch_bounds__(256) void combine16v_kernel(const uint16_t *__restr
     }
     const uint64_t o = (uint64_t)t * h + i;
     if (sh16) {
-        const float d = 1.0f + expf(-sh_gate[t]);
+        const float d = 1.0f + expf(-gate_input(sh_gate, gks, gridDim.y, t));
         const u32x4m r = *reinterpret_cast<const u32x4m *>(sh16 + o);
 #pragma unroll
         for (int q = 0; q < 4; q++) {
@@ -264,7 +274,7 @@ __global__ __launch_bounds__(256) void combine16v_kernel(const uint16_t *__restr
             v[2 * q + 1] = v[2 * q + 1] + bf16_hi(r[q]) / d;
         }
     } else if (sh_out) {
-        const float d = 1.0f + expf(-sh_gate[t]);
+        const float d = 1.0f + expf(-gate_input(sh_gate, gks, gridDim.y, t));
 #pragma unroll
         for (int j = 0; j < 8; j++) v[j] = v[j] + sh_out[o + j] / d;
     }
@@ -280,7 +290,7 @@ __global__ __launch_bounds__(256) void combine16v_kernel(const uint16_t *__restr
 hipError_t launch_combine16(Prof *p, hipStream_t s, const uint16_t *y16, const uint32_t *pos,
                             const float *wts, uint32_t k, const float *sh_out, const uint16_t *sh16,
                             const float *sh_gate, const float *resid, float *out, uint32_t tokens,
-                            uint32_t h) {
+                            uint32_t h, uint32_t gate_ks) {
     const bool vec = h % 8 == 0 &&
                      ((reinterpret_cast<uintptr_t>(y16) | reinterpret_cast<uintptr_t>(out) |
                        reinterpret_cast<uintptr_t>(sh16)) & 15u) == 0;
@@ -288,11 +298,11 @@ hipError_t launch_combine16(Prof *p, hipStream_t s, const uint16_t *y16, const u
         const uint32_t threads = h / 8 < 256 ? ((h / 8 + 63) / 64) * 64 : 256;
         dim3 grid((h / 8 + threads - 1) / threads, tokens);
         return launch_kernel(p, "combine16", combine16v_kernel, grid, dim3(threads), 0, s, y16, pos,
-                             wts, k, sh_out, sh16, sh_gate, resid, out, h);
+                             wts, k, sh_out, sh16, sh_gate, resid, out, h, gate_ks);
     }
     dim3 grid((h / 2 + 255) / 256, tokens);
     return launch_kernel(p, "combine16", combine16_kernel, grid, dim3(256), 0, s, y16, pos, wts, k,
-                         sh_out, sh16, sh_gate, resid, out, h);
+                         sh_out, sh16, sh_gate, resid, out, h, gate_ks);
 }
 
 hipError_t launch_identity_schedule(Prof *p, hipStream_t s, uint32_t rows, uint32_t tm, uint32_t *offsets,

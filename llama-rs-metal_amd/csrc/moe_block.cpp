@@ -47,10 +47,12 @@ WsLayout ws_layout(uint64_t T, uint64_t E, uint64_t K, uint64_t h, uint64_t ff, 
     take(L.eo, K * h);
     take(L.proj, h);
     take(L.sgv, 1);
-    // bf16 MFMA path (two bf16 per 4-byte element)
+    // bf16 MFMA path (two bf16 per 4-byte element); with a shared expert its
+    // T rows follow the T * K routed pairs in act16 and y16 (it runs as one
+    // more segment of the routed GEMMs where its kind allows)
     take(L.xb16, (T * h + 1) / 2);
-    take(L.act16, (T * K * ff + 1) / 2);
-    take(L.y16, (T * K * h + 1) / 2);
+    take(L.act16, (T * K * ff + T * (ffs > ff ? ffs : ff) * (ffs ? 1 : 0) + 1) / 2);
+    take(L.y16, (T * K * h + (ffs ? T * h : 0) + 1) / 2);
     take(L.tiles, 2 * ((T * K + 7) / 8 + E + 1));  // MFMA tiles of 128 pairs, batched runs of 8
     take(L.ntiles, 1);
     // the shared expert's one-segment schedule on the MFMA path: offsets [2],
@@ -102,9 +104,12 @@ moe_status check_block(moe_gpu *g, const moe_block_weights *w, Dims &d) {
     }
     if (d.E > 16384) return shape(g, "more than 16384 experts");
     // optional packed copies: sized for their weight, owned, disjoint from it
-    const moe_packed_weight *pk[3] = {&w->gate_packed, &w->up_packed, &w->down_packed};
-    const moe_weight *pw[3] = {&w->gate, &w->up, &w->down};
-    for (int i = 0; i < 3; i++) {
+    const moe_packed_weight *pk[6] = {&w->gate_packed,        &w->up_packed,        &w->down_packed,
+                                      &w->shared_gate_packed, &w->shared_up_packed, &w->shared_down_packed};
+    const moe_weight *pw[6] = {&w->gate, &w->up, &w->down, &w->shared_gate, &w->shared_up, &w->shared_down};
+    for (int i = 0; i < 6; i++) {
+        if (i >= 3 && !w->has_shared && (pk[i]->data.ptr || pk[i]->scales.ptr || pk[i]->biases.ptr))
+            return shape(g, "packed shared expert weights without a shared expert");
         if (!pk[i]->data.ptr && !pk[i]->scales.ptr && !pk[i]->biases.ptr) continue;
         uint64_t db = 0, sb = 0;
         if (!pack_layout(wdesc(*pw[i]), &db, &sb) || pk[i]->data.bytes != db || pk[i]->scales.bytes != sb ||
@@ -114,6 +119,8 @@ moe_status check_block(moe_gpu *g, const moe_block_weights *w, Dims &d) {
     }
     if (!w->gate_packed.data.ptr != !w->up_packed.data.ptr)
         return shape(g, "packed expert weights: gate and up together");
+    if (!w->shared_gate_packed.data.ptr != !w->shared_up_packed.data.ptr)
+        return shape(g, "packed shared expert weights: gate and up together");
     return MOE_OK;
 }
 
@@ -352,6 +359,18 @@ moe_status run_mfma(moe_gpu *g, const moe_block_weights *w, const Dims &d, const
     const float *xin = nw ? xn : xraw;  // F32 input of the router and the VALU products
     const WDesc R = wdesc(w->router);
     const float *bias = has(io->logit_bias) ? fp(io->logit_bias) : nullptr;
+    // The shared expert as one more segment of the routed experts' GEMMs
+    // (its rows after the T * K pairs of act16 / y16) when its weights are of
+    // their kind and width; its gate input then comes from the router's own
+    // pass over x when it is a dense F32 row (gate_ks partial sums in sh_act).
+    const bool fold = w->has_shared &&
+                      gemm_shared_fold_ok(wdesc(w->gate), wdesc(w->up), wdesc(w->down), wdesc(w->shared_gate),
+                                          wdesc(w->shared_up), wdesc(w->shared_down), T, K);
+    const WDesc GI = fold ? gate_inp_desc(w->shared_gate_inp) : WDesc{};
+    bool gate_in_router = fold && GI.bits == 0 && GI.type == 0 && aligned16(GI.data) &&
+                          f32mm_supported(R, xin);
+    float *gparts = ws + L.sh_act;  // [ks][T] (T * ffs floats, unused by the folded path)
+    uint32_t gate_ks = 1;
     // the router product stays F32 (the routing is exact given the logits);
     // only the expert products run in bf16.  `x16`: the router also rounds x
     // to bf16 for them (one pass over x where there is no norm to apply).
@@ -361,12 +380,19 @@ moe_status run_mfma(moe_gpu *g, const moe_block_weights *w, const Dims &d, const
             float *parts = reinterpret_cast<float *>(y16);
             const uint64_t part_floats = (uint64_t)T * K * d.h / 2;
             const uint32_t ks = f32mm_ksplit(R, (uint32_t)T, part_floats);
+            // the gate row's K range fits the router's LDS, and its partial sums sh_act
+            if (gate_in_router &&
+                (d.h / ks > f32mm_gate_max() || (uint64_t)ks * f32mm_columns(R) > d.ffs))
+                gate_in_router = false;
+            const float *grow = gate_in_router ? static_cast<const float *>(GI.data) : nullptr;
+            float *gout = gate_in_router ? gparts : nullptr;
+            gate_ks = gate_in_router ? ks * f32mm_columns(R) : 1u;
             if (ks > 1) {
-                TRY(launch_f32mm(p, s, "router_f32", R, xin, (uint32_t)T, ks, nullptr, parts, x16));
+                TRY(launch_f32mm(p, s, "router_f32", R, xin, (uint32_t)T, ks, nullptr, parts, x16, grow, gout));
                 TRY(launch_route_sum(p, s, parts, ks, bias, E, K, w->normalize ? 1 : 0, (uint32_t)T,
                                      logits, ids, wts));
             } else {
-                TRY(launch_f32mm(p, s, "router_f32", R, xin, (uint32_t)T, 1, bias, logits, x16));
+                TRY(launch_f32mm(p, s, "router_f32", R, xin, (uint32_t)T, 1, bias, logits, x16, grow, gout));
                 TRY(launch_route(p, s, logits, E, K, w->normalize ? 1 : 0, (uint32_t)T, ids, wts));
             }
         } else {
@@ -382,6 +408,34 @@ moe_status run_mfma(moe_gpu *g, const moe_block_weights *w, const Dims &d, const
         if (st != MOE_OK) return st;
     } else {
         TRY(launch_to_bf16(p, s, xraw, nw, eps, (uint32_t)T, (uint32_t)d.h, xb16, xn));
+    }
+    if (fold) {
+        // one stream: router, dispatch, the GEMMs over the routed segments
+        // and the shared segment, the combine
+        if (!router_rounds) {
+            const moe_status st = router(nullptr);
+            if (st != MOE_OK) return st;
+        }
+        const float *sgv = gparts;
+        if (!gate_in_router) {
+            float *sgt = ws + L.sh_gate;
+            TRY(launch_gemv(p, s, gate_inp_desc(w->shared_gate_inp), xin, 0, nullptr, 1, sgt, (uint32_t)T));
+            sgv = sgt;
+            gate_ks = 1;
+        }
+        TRY(launch_dispatch(p, s, ids, (uint32_t)(T * K), E, counts, offsets, perm, pos, gemm_tile_rows(), tiles,
+                            ntiles));
+        const uint32_t base = (uint32_t)(T * K);
+        const SharedSeg sh_gu{wdesc(w->shared_gate), wdesc(w->shared_up), packed(w->shared_gate_packed),
+                              packed(w->shared_up_packed), (uint32_t)T, base};
+        const SharedSeg sh_dn{wdesc(w->shared_down), wdesc(w->shared_down), packed(w->shared_down_packed),
+                              packed(w->shared_down_packed), (uint32_t)T, base};
+        TRY(launch_mfma_experts(p, s, wdesc(w->gate), wdesc(w->up), wdesc(w->down), packed(w->gate_packed),
+                                packed(w->up_packed), packed(w->down_packed), xb16, (uint32_t)T, offsets, perm, K,
+                                tiles, ntiles, act16, y16, &sh_gu, &sh_dn));
+        TRY(launch_combine16(p, s, y16, pos, wts, K, nullptr, y16 + (uint64_t)base * d.h, sgv,
+                             io->residual ? xraw : nullptr, out, (uint32_t)T, (uint32_t)d.h, gate_ks));
+        return MOE_OK;
     }
     // The shared expert needs only the input: on the side stream from here,
     // alongside the router product (when that does not produce the bf16

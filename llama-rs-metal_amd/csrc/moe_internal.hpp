@@ -94,9 +94,15 @@ hipError_t launch_route_sum(Prof *p, hipStream_t s, const float *parts, uint32_t
 bool f32mm_supported(const WDesc &w, const float *x);
 uint32_t f32mm_ksplit(const WDesc &w, uint32_t tokens, uint64_t part_floats);
 // xb16 (optional, [tokens, in]): x rounded to bf16, written on the way.
+// grow: a dense F32 row (16-byte aligned) whose product with every token's x
+// the router also forms, one partial sum per K range and column of 128
+// outputs: gout[(kr * f32mm_columns(w) + c) * tokens + t]; a K range
+// (w.in / ksplit) of at most f32mm_gate_max() values
+uint32_t f32mm_gate_max();
+uint32_t f32mm_columns(const WDesc &w);
 hipError_t launch_f32mm(Prof *p, hipStream_t s, const char *name, const WDesc &w, const float *x,
                         uint32_t tokens, uint32_t ksplit, const float *bias, float *out,
-                        uint16_t *xb16 = nullptr);
+                        uint16_t *xb16 = nullptr, const float *grow = nullptr, float *gout = nullptr);
 hipError_t launch_route(Prof *p, hipStream_t s, const float *logits, uint32_t experts, uint32_t k,
                         int normalize, uint32_t tokens, uint32_t *ids, float *weights);
 // With `tiles` it also writes the work list of tm-pair runs that
@@ -156,6 +162,16 @@ hipError_t launch_to_bf16(Prof *p, hipStream_t s, const float *x, const float *n
 struct PackedW {
     const void *data, *scales, *biases;
 };
+// One more segment of the grouped GEMM after the routed experts' (the
+// shared expert): its weights (w2: up, for gate/up), their packed copies
+// (null data: none), and its rows [base, base + rows) of the output and, for
+// the down product, of the A rows (the gate/up product reads A row r - base,
+// i.e. the token's own row).
+struct SharedSeg {
+    WDesc w, w2;
+    PackedW pk, pk2;
+    uint32_t rows, base;
+};
 // Byte sizes of the packed copy (false: no packed form -- affine weights with
 // 16-bit scales, in % 128 == 0, offsets below 2^32 only).
 bool pack_layout(const WDesc &w, uint64_t *data_bytes, uint64_t *sb_bytes);
@@ -163,11 +179,14 @@ hipError_t launch_pack_weight(Prof *p, hipStream_t s, const WDesc &w, void *data
                               void *biases);
 // tiles / ntiles: the work list of gemm_tile_rows()-pair M-tiles, written by
 // launch_dispatch (or launch_tile_schedule) over the same offsets.
+// sh_gu / sh_dn: the shared expert as one more segment of the gate/up and
+// down GEMMs (null: none); its rows follow the T*k routed pairs in act16 and y16.
 hipError_t launch_mfma_experts(Prof *p, hipStream_t s, const WDesc &gate, const WDesc &up,
                                const WDesc &down, const PackedW &pg, const PackedW &pu,
                                const PackedW &pd, const uint16_t *xb16, uint32_t tokens,
                                const uint32_t *offsets, const uint32_t *perm, uint32_t k,
-                               uint32_t *tiles, uint32_t *ntiles, uint16_t *act16, uint16_t *y16);
+                               uint32_t *tiles, uint32_t *ntiles, uint16_t *act16, uint16_t *y16,
+                               const SharedSeg *sh_gu = nullptr, const SharedSeg *sh_dn = nullptr);
 // Grouped expert GEMM over the dispatched segments (k_gemm.hip): down = 0 for
 // gate/up + SwiGLU (w = gate, w2 = up, a_rows = xb16, out = act16), 1 for the
 // down product (w = w2 = down, a_rows = act16, out = y16; the combine applies
@@ -176,22 +195,30 @@ hipError_t launch_mfma_experts(Prof *p, hipStream_t s, const WDesc &gate, const 
 // tile_schedule.
 bool gemm_supported(const WDesc &w);
 uint32_t gemm_tile_rows();  // pairs per work item (the M-tiles tile_schedule emits)
+// Whether the shared expert (sg/su/sd) can run as that segment of the routed
+// experts' affine GEMMs (g/u/d) over T tokens x K: the same code width,
+// scale type and group, the same intermediate width, and every offset within
+// 32 bits.
+bool gemm_shared_fold_ok(const WDesc &g, const WDesc &u, const WDesc &d, const WDesc &sg, const WDesc &su,
+                         const WDesc &sd, uint64_t T, uint64_t K);
 // pk, pk2: packed copies of w, w2 (PackedW with null data: none).
 // perm null: pair p is row p of a_rows (one segment of all rows, the shared
-// expert).  `name`: the profile name (null: gemm_gateup / gemm_down).
+// expert).  sh: the shared expert as one more segment (null: none).  `name`:
+// the profile name (null: gemm_gateup / gemm_down).
 hipError_t launch_grouped_gemm(Prof *p, hipStream_t s, int down, const WDesc &w, const WDesc &w2,
                                const PackedW &pk, const PackedW &pk2, const uint16_t *a_rows,
                                uint64_t a_rows_n, const uint32_t *perm, const uint32_t *offsets,
                                const uint32_t *tiles, const uint32_t *ntiles, uint32_t k,
-                               uint16_t *out, const char *name = nullptr);
+                               uint16_t *out, const char *name = nullptr, const SharedSeg *sh = nullptr);
 // offsets {0, rows}, the M-tiles of tm rows over them, and their count
 hipError_t launch_identity_schedule(Prof *p, hipStream_t s, uint32_t rows, uint32_t tm, uint32_t *offsets,
                                     uint32_t *tiles, uint32_t *ntiles);
-// the shared expert's output as F32 (sh_out) or bf16 (sh16), or neither
+// the shared expert's output as F32 (sh_out) or bf16 (sh16), or neither; its
+// gate input sh_gate[t], or the sum of gate_ks partial sums sh_gate[kr * tokens + t]
 hipError_t launch_combine16(Prof *p, hipStream_t s, const uint16_t *y16, const uint32_t *pos,
                             const float *wts, uint32_t k, const float *sh_out, const uint16_t *sh16,
                             const float *sh_gate, const float *resid, float *out, uint32_t tokens,
-                            uint32_t h);
+                            uint32_t h, uint32_t gate_ks = 1);
 
 // ---- batched decode (k_batched.hip) ----
 // Row products over work entries of at most seg_tokens() input rows: entries

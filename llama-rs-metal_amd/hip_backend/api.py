@@ -99,6 +99,9 @@ class MoeBlockWeightsC(C.Structure):
         ("gate_packed", MoePackedWeightC),
         ("up_packed", MoePackedWeightC),
         ("down_packed", MoePackedWeightC),
+        ("shared_gate_packed", MoePackedWeightC),
+        ("shared_up_packed", MoePackedWeightC),
+        ("shared_down_packed", MoePackedWeightC),
     ]
 
 
@@ -302,11 +305,16 @@ class BlockWeights:
     """FeedForward::Moe (crates/model-runtime/src/lib.rs:46-56)."""
 
     def __init__(self, router, gate, up, down, experts_used, normalize, shared=None,
-                 shared_gate=None, packed=None):
+                 shared_gate=None, packed=None, shared_packed=None):
         c = MoeBlockWeightsC()
         c.router, c.gate, c.up, c.down = router.c, gate.c, up.c, down.c
         if packed is not None:  # PackedWeight copies of (gate, up, down), any of them None
             for name, pw in zip(("gate_packed", "up_packed", "down_packed"), packed):
+                if pw is not None:
+                    setattr(c, name, pw.c)
+        if shared_packed is not None:  # the same for the shared expert's (gate, up, down)
+            for name, pw in zip(("shared_gate_packed", "shared_up_packed", "shared_down_packed"),
+                                shared_packed):
                 if pw is not None:
                     setattr(c, name, pw.c)
         if shared is not None:
@@ -318,6 +326,7 @@ class BlockWeights:
         self.c = c
         self.keep = (router, gate, up, down, shared, shared_gate)
         self.packed = packed
+        self.shared_packed = shared_packed
         self.hidden = router.dims[0]
         self.experts = router.dims[1]
         self.k = experts_used

@@ -833,6 +833,71 @@ def test_config4_routing_matches_oracle_f32_logits(gpu, c4):
     np.testing.assert_allclose(got[3][clear], ref_w[clear], rtol=1e-5, atol=1e-8)
 
 
+@pytest.mark.parametrize("gate_kind,packed,norm,T", [(DENSE, "all", False, 300), (DENSE, "routed", True, 300),
+                                                     (DENSE, "none", False, 2048), ((8, 64, BF16), "all", True, 130),
+                                                     (DENSE, "shared", False, 64)])
+def test_mfma_path_shared_expert_folded(gpu, gate_kind, packed, norm, T):
+    """A shared expert of the routed experts' kind and width runs as one more
+    segment of the routed experts' bf16 GEMMs (its rows after the T*K pairs,
+    spread over the item order), with no side stream, identity schedule or
+    separate shared GEMMs; a dense F32 gate row is multiplied inside the
+    router's pass over x (partial sums per K range), other gate kinds keep
+    their one-row product.  Every token against the oracle at the bf16
+    tolerance, with and without packed copies (of the routed experts, of the
+    shared expert, of both), the RMSNorm input path and the residual; the
+    packed runs equal the row-major run bit for bit."""
+    print(f"[case] MFMA shared folded gate={gate_kind} packed={packed} norm={norm} T={T}", flush=True)
+    kinds = {"router": DENSE, "experts": (4, 64, BF16), "shared": (4, 64, BF16), "shared_gate": gate_kind}
+    blk = HostBlock(256, 16, 4, 128, 128, kinds, seed=107, random_experts=True)
+    bw = blk.upload(gpu)
+    router, gate, up, down, shared, sg = bw.keep
+    pk = [gpu.pack_weight(w) for w in (gate, up, down)] if packed in ("all", "routed") else None
+    spk = [gpu.pack_weight(w) for w in shared] if packed in ("all", "shared") else None
+    bwp = BlockWeights(router, gate, up, down, bw.k, True, shared, sg, packed=pk, shared_packed=spk)
+    x = synth.normal(5500 + T, T * 256).reshape(T, 256)
+    nw = (1.0 + 0.1 * synth.normal(5501, 256)).astype(np.float32) if norm else None
+    bias = hot_bias(T, 16, seed=T, frac=0.5, hot=3, boost=4.0)
+    gpu.profile_reset()
+    gpu.profile(True)
+    got = run_block(gpu, bwp, x, T, PATH_MFMA, bias=bias, norm_w=nw, residual=True)
+    prof = gpu.profile_read()
+    gpu.profile(False)
+    for name in ("gemm_shared_gateup", "gemm_shared_down", "identity_schedule"):
+        assert name not in prof, sorted(prof)
+    assert ("gemv_row1" in prof) == (gate_kind != DENSE), sorted(prof)
+    check_all_ids(blk, got)
+    check_against_oracle(blk, x, got, bias=bias, tol=BF16_TOL, norm_w=nw, residual=True)
+    if packed != "none":
+        ref = run_block(gpu, bw, x, T, PATH_MFMA, bias=bias, norm_w=nw, residual=True)
+        assert np.array_equal(got[2], ref[2])
+        assert np.array_equal(got[0], ref[0])
+    for pw in (pk or []) + (spk or []):
+        for b in pw.buffers:
+            gpu.release(b)
+
+
+def test_packed_shared_copies_are_validated(gpu):
+    """moe_block refuses packed shared-expert copies without a shared expert,
+    or a shared gate copy without the shared up copy."""
+    kinds = {"router": DENSE, "experts": (4, 64, BF16), "shared": (4, 64, BF16), "shared_gate": DENSE}
+    blk = HostBlock(256, 8, 2, 128, 128, kinds, seed=108, random_experts=True)
+    bw = blk.upload(gpu)
+    router, gate, up, down, shared, sg = bw.keep
+    spk = [gpu.pack_weight(w) for w in shared]
+    x = gpu.upload(synth.normal(5600, 64 * 256))
+    out = gpu.zeros(64 * 256)
+    for bad in (BlockWeights(router, gate, up, down, 2, True, shared_packed=spk),
+                BlockWeights(router, gate, up, down, 2, True, shared, sg, shared_packed=[spk[0], None, spk[2]])):
+        ws = gpu.zeros(bad.workspace_elems(64))
+        with pytest.raises(ShapeError):
+            with gpu.batch() as b:
+                b.moe_block(bad, x, out, 64, ws, path=PATH_MFMA)
+        gpu.release(ws)
+    for pw in spk:
+        for b in pw.buffers:
+            gpu.release(b)
+
+
 @pytest.mark.parametrize("shared,ffs,on_gemm", [((8, 32, BF16), 256, True), ((4, 64, F16), 256, True),
                                                 (DENSE, 256, True), ((4, 64, BF16), 192, False)])
 def test_mfma_path_shared_expert_kinds(gpu, shared, ffs, on_gemm):
