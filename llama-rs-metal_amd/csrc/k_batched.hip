@@ -17,7 +17,7 @@
 //
 // Entries: either the dispatch's segments cut into runs of kSegTokens pairs
 // (tile_schedule: (expert, first pair); the run ends at the segment end), or
-// runs of kSegRun rows over [0, n) of a single weight.
+// runs of seg_run(n) rows over [0, n) of a single weight.
 #include "lanerows.hpp"
 #include "rowdot.hpp"
 
@@ -26,8 +26,11 @@ namespace moehip {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kSegTokens = 8;  // pairs per work entry over the dispatched segments
-constexpr uint32_t kSegRun = 2;     // input rows per entry over all tokens (router, shared
-                                    // expert): small weights, so more waves beat re-reads
+// Input rows per entry over all tokens (router, shared expert): the weights
+// are small, so more waves beat re-reads at a few tokens; from 48 tokens on,
+// runs of 4 (config 3 at 64 tokens: 271.5 -> 262.4 us per step; at 8 tokens
+// runs of 4 cost 72.8 -> 75.6 us).
+__host__ __device__ inline uint32_t seg_run(uint32_t n) { return n >= 48 ? 4u : 2u; }
 constexpr int kSegGateItems = 2;    // kGateFR-row items of gate (and of up) rows per wave
 constexpr int kSegRowsFR = 4;       // row instructions per wave in seg_rows
 
@@ -40,6 +43,7 @@ struct SegArgs {
     const uint32_t *ntiles;   // entry count (device), with tiles
     const uint32_t *offsets;  // segment ends offsets[e + 1], with tiles
     uint32_t n;               // without tiles: input rows
+    uint32_t run;             // without tiles: input rows per entry (seg_run(n))
     const float *bias;        // seg_rows: added to out[p, row] (or nullptr)
     float *out;               // [p, w.out]
 };
@@ -54,9 +58,9 @@ __device__ __forceinline__ bool seg_entry(const SegArgs &a, uint32_t i, uint32_t
         end = min(a.offsets[e + 1], beg + kSegTokens);
     } else {
         e = 0;
-        beg = i * kSegRun;
+        beg = i * a.run;
         if (beg >= a.n) return false;
-        end = min(a.n, beg + kSegRun);
+        end = min(a.n, beg + a.run);
     }
     return true;
 }
@@ -269,7 +273,7 @@ static bool chunk_rows_ok(const WDesc &w) {
 bool seg_supported(const WDesc &w) { return chunk_rows_ok(w); }
 
 uint32_t seg_max_entries(uint32_t pairs, uint32_t experts) {
-    if (experts == 0) return (pairs + kSegRun - 1) / kSegRun;
+    if (experts == 0) return (pairs + seg_run(pairs) - 1) / seg_run(pairs);
     return (pairs + kSegTokens - 1) / kSegTokens + (experts < pairs ? experts : pairs);
 }
 uint32_t seg_tokens() { return kSegTokens; }
@@ -322,6 +326,7 @@ hipError_t launch_seg_gateup(Prof *p, hipStream_t s, const char *name, const WDe
     a.ntiles = ntiles;
     a.offsets = offsets;
     a.n = n;
+    a.run = seg_run(n);
     a.out = act;
     return dispatch_kind(gate, SegLaunch<1>{p, s, a, entries, name});
 }
@@ -339,6 +344,7 @@ hipError_t launch_seg_rows(Prof *p, hipStream_t s, const char *name, const WDesc
     a.ntiles = ntiles;
     a.offsets = offsets;
     a.n = n;
+    a.run = seg_run(n);
     a.bias = bias;
     a.out = out;
     return dispatch_kind(w, SegLaunch<0>{p, s, a, entries, name});
