@@ -142,9 +142,10 @@ __global__ __launch_bounds__(kThreads) void f32mm_kernel(WDesc r, const float *_
     f32x4 xr[2][2];  // native vectors: HIP's float4 struct would stay in scratch
     WRaw<BITS, T> wr[2];
     // shared-gate row (GATE): the block's K range of it goes to LDS once
-    // (klen <= kGateMax, checked on the host); every thread multiplies the x
-    // values it stages with the matching gate values (no loads in the loop,
-    // no branch); the first expert column stores the sums
+    // (klen <= kGateMax, checked on the host); in the iterations its expert
+    // column takes, every thread multiplies the x values it stages with the
+    // matching gate values (no loads in the loop; the branch is uniform), and
+    // every column stores its partial sums
     float gsum = 0.f;
     if constexpr (GATE) {
         for (uint32_t k = 4 * tid; k < klen; k += 4 * kThreads)
