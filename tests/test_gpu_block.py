@@ -255,12 +255,13 @@ def c3(gpu):
     return blk, blk.upload(gpu)
 
 
-@pytest.mark.parametrize("T", [1, 8, 32, 64])
+@pytest.mark.parametrize("T", [1, 8, 32, 50, 64])
 def test_config3_mixed_precision_hot_set(gpu, c3, T):
     """Config 3 through AUTO (fused decode at 1 token, the batched decode with
     the fused route + dispatch launch above): every token's ids and output
     against the oracle, and the dispatch and 8-pair work list built inside
-    the block against orc_dispatch."""
+    the block against orc_dispatch.  From 48 tokens the all-token products
+    run over entries of 4 input rows; at 50 the last entry holds 2."""
     blk, bw = c3
     print(f"[case] config3 T={T}", flush=True)
     x = synth.normal(2000 + T, T * 2048).reshape(T, 2048)
